@@ -1,0 +1,267 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark of the MI355X attention block (one GPU).
+
+Default workload: one decode step of the Llama-3-8B attention block at an
+8K context -- H32 / HK8 / D128, 8192 cached rows per layer in an fp32 KV
+cache, RoPE theta 5e5, new token at position 8192 -- over all 32 layers back
+to back, each layer with its own cache (2.15 GB in HBM).  A "step" is those
+32 layer calls of pkh_attn_decode_async, each doing RoPE on q/k, the KV
+append and GQA attention over 8193 rows.
+
+Prints one JSON line.  `value` is whole-job KV throughput in GB/s from the
+algorithmic bytes per layer-step
+    2*(ctx+1)*HK*D*s_kv + 2*H*D*4 + 2*HK*D*(4 + s_kv)
+(KV stream, q in, o out, new k/v in, appended row out) over the timed wall
+time.  `roofline.achieved` is the same bytes over the average duration of one
+layer call measured with HIP events on the launch stream.  `cpu_baseline` is
+the oracle's restatement of the reference's OpenMP attention path timed on
+this host's cores over a bounded sample of the same workload.
+
+Inputs are synthetic: N(0,1) from torch's CUDA generator seeded with the
+workload's seed, already resident in HBM when timing starts.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode-attn KV GB/s (% HBM peak) + µs/layer-step, Llama-3-8B shape ctx 8K"
+HBM_PEAK_GBS = 8000.0
+
+WORKLOADS = {
+    "llama3-8b-decode-ctx8192": dict(H=32, HK=8, D=128, ctx=8192, theta=5e5, layers=32,
+                                     kv="f32", seed=3),
+    "tinyllama-decode-ctx2048": dict(H=32, HK=4, D=64, ctx=2048, theta=1e4, layers=1,
+                                     kv="f32", seed=2),
+    "tinyllama-decode-ctx2048-rotating64": dict(H=32, HK=4, D=64, ctx=2048, theta=1e4,
+                                                layers=64, kv="f32", seed=2),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def decode_bytes(ctx: int, H: int, HK: int, D: int, s_kv: int) -> int:
+    return 2 * (ctx + 1) * HK * D * s_kv + 2 * H * D * 4 + 2 * HK * D * (4 + s_kv)
+
+
+def traffic_from_profiles(workload: str):
+    """HBM bytes per launch measured with rocprofv3 PMC counters (FETCH_SIZE,
+    WRITE_SIZE) and scaled by a plain copy kernel's reading, if recorded."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        t = json.load(open(path)).get(workload)
+        return None if t is None else float(t["bytes_per_launch"])
+    except (ValueError, KeyError, TypeError):
+        return None
+
+
+def cpu_baseline_decode(K, V, q, k, v, cfg, layers, threads):
+    """The oracle (the reference's OpenMP-over-heads attention, restated) on
+    host copies of `layers` layers: one warm-up layer call, then one timed
+    decode step over those layers."""
+    from oracle import pyoracle as po
+    H, HK, D, ctx = cfg["H"], cfg["HK"], cfg["D"], cfg["ctx"]
+    _, sin, cos = po.rope_tables(D, cfg["theta"], ctx + 1)
+    host = [(K[L].cpu().numpy(), V[L].cpu().numpy(), q[L].cpu().numpy(), k[L].cpu().numpy(),
+             v[L].cpu().numpy()) for L in range(layers)]
+    kc, vc, qq, kk, vv = host[0]
+    po.decode_step(kc, vc, ctx, qq, kk, vv, sin, cos, threads)     # warm-up
+    t0 = time.perf_counter()
+    for kc, vc, qq, kk, vv in host:
+        po.decode_step(kc, vc, ctx, qq, kk, vv, sin, cos, threads)
+    return (time.perf_counter() - t0) / layers
+
+
+def run_decode(args, cfg):
+    import torch
+    import lestramanika_amd as pk
+    from oracle import pyoracle as po
+
+    torch.cuda.set_device(0)
+    lib = pk.load()
+    pk.check(lib.pkh_init(0), "pkh_init")
+    H, HK, D, ctx, L = cfg["H"], cfg["HK"], cfg["D"], cfg["ctx"], cfg["layers"]
+    max_seq = ctx + 1
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(cfg["seed"])
+    log(f"bench: allocating {L} layers x {max_seq} rows x {HK}x{D} fp32 K and V")
+    K = torch.zeros((L, max_seq, HK, D), dtype=torch.float32, device=dev)
+    V = torch.zeros((L, max_seq, HK, D), dtype=torch.float32, device=dev)
+    for layer in range(L):
+        K[layer, :ctx].normal_(generator=gen)
+        V[layer, :ctx].normal_(generator=gen)
+    q = torch.randn((L, H, D), generator=gen, device=dev)
+    k = torch.randn((L, HK, D), generator=gen, device=dev)
+    v = torch.randn((L, HK, D), generator=gen, device=dev)
+    ao = torch.zeros((L, H, D), device=dev)
+
+    # The cache struct points at torch's buffers (pkh_kv_t is caller-owned,
+    # as pickle_fast_kv_t is).
+    kv = pk.KV()
+    kv.n_layers, kv.n_kv_heads, kv.head_dim, kv.max_seq = L, HK, D, max_seq
+    kv.k_stride_layer = kv.v_stride_layer = max_seq * HK * D
+    kv.k, kv.v, kv.dtype, kv.device = K.data_ptr(), V.data_ptr(), pk.PKH_KV_F32, 0
+
+    half = min(D // 2, 64)
+    sin = np.zeros((max_seq, half), np.float32)
+    cos = np.zeros((max_seq, half), np.float32)
+    lib.pkh_rope_host_tables(D, cfg["theta"], 0, ctx, None, sin.ctypes.data, cos.ctypes.data)
+    rope = pk.Rope()
+    pk.check(lib.pkh_rope_alloc(max_seq, half, ctypes.byref(rope)), "pkh_rope_alloc")
+    pk.check(lib.pkh_rope_upload(ctypes.byref(rope), sin.ctypes.data, cos.ctypes.data, max_seq),
+             "pkh_rope_upload")
+
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    kvp, rp = ctypes.byref(kv), ctypes.byref(rope)
+    qp = [q[i].data_ptr() for i in range(L)]
+    kp = [k[i].data_ptr() for i in range(L)]
+    vp = [v[i].data_ptr() for i in range(L)]
+    op = [ao[i].data_ptr() for i in range(L)]
+    call = lib.pkh_attn_decode_async
+
+    def step(events=None):
+        for layer in range(L):
+            if events is not None:
+                events[layer][0].record(stream)
+            rc = call(kvp, rp, layer, ctx, H, qp[layer], kp[layer], vp[layer], op[layer], sp)
+            if rc != 0:
+                raise pk.PkhError(rc, "pkh_attn_decode_async")
+            if events is not None:
+                events[layer][1].record(stream)
+
+    log(f"bench: warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region 1: wall time of exactly K back-to-back steps.
+    log(f"bench: timing {args.steps} steps x {L} layers")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    # Timed region 2: the same launches bracketed by HIP events on the launch
+    # stream, for the per-launch kernel duration.
+    evs = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+            for _ in range(L)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for s in range(args.steps):
+        step(evs[s])
+    torch.cuda.synchronize()
+    durs = np.array([e0.elapsed_time(e1) for st in evs for e0, e1 in st]) * 1e-3  # s
+
+    s_kv = 4
+    bpl = decode_bytes(ctx, H, HK, D, s_kv)
+    n_launch = args.steps * L
+    value = bpl * n_launch / wall / 1e9
+    avg_launch = float(durs.mean())
+    achieved = bpl / avg_launch / 1e9
+
+    # Parity of the benchmarked outputs (first and last layer) against the oracle.
+    _, osin, ocos = po.rope_tables(D, cfg["theta"], max_seq)
+    errs = []
+    for layer in sorted({0, L - 1}):
+        ref, _, _ = po.decode_step(K[layer].cpu().numpy(), V[layer].cpu().numpy(), ctx,
+                                   q[layer].cpu().numpy(), k[layer].cpu().numpy(),
+                                   v[layer].cpu().numpy(), osin, ocos, n_threads=16)
+        errs.append(float(np.max(np.abs(ao[layer].cpu().numpy() - ref))))
+    log(f"bench: max-abs err vs oracle (layers 0, {L - 1}): {max(errs):.3e}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        sample_layers = min(L, args.cpu_layers)
+        log(f"bench: CPU baseline (oracle, {threads} threads, {sample_layers} layers)")
+        t_cpu = cpu_baseline_decode(K, V, q, k, v, cfg, sample_layers, threads)
+        cpu = {"value": round(bpl / t_cpu / 1e9, 3), "unit": "GB/s", "cores": threads,
+               "kind": "port",
+               "sample": (f"one decode step over {sample_layers} layer(s) of the same workload "
+                          f"({ctx} cached rows each) with the oracle's restatement of the "
+                          f"reference's OpenMP-over-heads attention (oracle/pk_oracle.c)"),
+               "us_per_layer_step": round(t_cpu * 1e6, 2)}
+
+    lib.pkh_rope_free(rp)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: N(0,1) from torch's CUDA generator, seeded per workload",
+        "config": {"workload": args.workload, "n_heads": H, "n_kv_heads": HK, "head_dim": D,
+                   "context": ctx, "layers": L, "kv_dtype": cfg["kv"],
+                   "rope_theta": cfg["theta"], "new_token_pos": ctx},
+        "us_per_layer_step": round(wall / n_launch * 1e6, 3),
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "bytes_per_layer_step": bpl,
+        "max_abs_err_vs_oracle": max(errs),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles(args.workload),
+                     "kernel_us": round(avg_launch * 1e6, 3)},
+        "cpu_baseline": cpu,
+    }
+    return result
+
+
+def run_copy_calibration(args):
+    """A plain device copy of known size, for scaling the PMC byte counters."""
+    import torch
+    n = 256 << 20   # 1 GiB of fp32
+    a = torch.randn(n, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(args.warmup + args.steps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4,
+                      "launches": args.warmup + args.steps}), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="llama3-8b-decode-ctx8192",
+                    choices=sorted(WORKLOADS) + ["copy-calibration"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=32,
+                    help="layers in the CPU-baseline sample")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path)", file=sys.stderr)
+        sys.exit(2)
+    if args.workload == "copy-calibration":
+        run_copy_calibration(args)
+        return
+    res = run_decode(args, WORKLOADS[args.workload])
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

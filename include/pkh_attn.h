@@ -1,0 +1,229 @@
+/*
+ * pkh_attn.h -- C ABI of the MI355X (gfx950) attention block for pickle's
+ * fast path: RoPE on Q/K, KV-cache append and grouped-query attention for
+ * single-sequence decode, causal prefill and ragged multi-sequence decode.
+ *
+ * The reference has no operator seam for attention: it is inline code inside
+ * pickle_fast_forward (src/pickle_fast.c:1910-2094).  These entry points are
+ * what that inline block calls instead; every declaration names the
+ * reference code it replaces.  Plain C types and pointers only.
+ *
+ * Conventions (the reference's, src/pickle.h:52-60, src/pickle_fast.c:1816):
+ *   - functions return PKH_OK (0) or a negative code with the same value as
+ *     the matching PICKLE_ERR_* constant, and never abort;
+ *   - *_alloc fills a caller-owned struct, *_free releases it and zeroes it;
+ *   - one host thread calls in; nothing here is reentrant;
+ *   - "_async" entry points take device pointers and a hipStream_t passed as
+ *     void* (NULL = the null stream), enqueue work and return; the others
+ *     take host pointers and return when the result is in host memory.
+ *
+ * Layouts (fp32 values unless stated):
+ *   q   [n_heads][head_dim]           ao  [n_heads][head_dim]
+ *   k,v [n_kv_heads][head_dim]        (the reference's state->q/k/v/ao,
+ *                                      src/pickle_fast.h:107-110)
+ *   KV  [layer][pos][kv_head][head_dim], fp32 or fp16, in device memory
+ *       (the reference's layout, src/pickle_fast.c:1940-1942)
+ *   query head h reads KV head h * n_kv_heads / n_heads
+ *   (src/pickle_fast.c:1963); n_heads must be a multiple of n_kv_heads.
+ *
+ * Supported shapes: head_dim in {16, 32, 64, 128, 256}; group size
+ * n_heads / n_kv_heads in {1, 2, 4, 8} (head_dim 256: group <= 4).  Others
+ * return PKH_ERR_ARG.
+ */
+#ifndef PKH_ATTN_H
+#define PKH_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: same values as src/pickle.h:52-60. */
+#define PKH_OK          0
+#define PKH_ERR_MEMORY -3   /* device allocation failed           */
+#define PKH_ERR_IO     -5   /* HIP runtime or launch failure       */
+#define PKH_ERR_ARG    -6   /* bad argument or unsupported shape   */
+#define PKH_ERR_RANGE  -7   /* position or layer out of range      */
+
+/* KV element types: the ggml_type values of src/pickle.h:85-87. */
+#define PKH_KV_F32 0
+#define PKH_KV_F16 1
+
+/* ------------------------------------------------------------------ */
+/* Library                                                            */
+/* ------------------------------------------------------------------ */
+
+/* Select the HIP device used by every later call (default 0).  Optional. */
+int pkh_init(int device);
+
+/* Version string of this library. */
+const char* pkh_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Device KV cache                                                    */
+/* ------------------------------------------------------------------ */
+
+/* Device-resident mirror of pickle_fast_kv_t (src/pickle_fast.h:145-154):
+ * the first eight fields have the reference's names and meaning (strides
+ * are in elements); k and v are device pointers of element type dtype. */
+typedef struct {
+    int    n_layers;
+    int    n_kv_heads;
+    int    head_dim;
+    int    max_seq;
+    size_t k_stride_layer;   /* max_seq * n_kv_heads * head_dim */
+    size_t v_stride_layer;
+    void*  k;                /* device [n_layers * k_stride_layer] */
+    void*  v;                /* device [n_layers * v_stride_layer] */
+    int    dtype;            /* PKH_KV_F32 or PKH_KV_F16 */
+    int    device;
+} pkh_kv_t;
+
+/* Replaces pickle_fast_kv_alloc (src/pickle_fast.c:1793-1810): two zeroed
+ * device buffers of n_layers * max_seq * n_kv_heads * head_dim elements.
+ * PKH_ERR_MEMORY if the device cannot hold them (the struct is zeroed). */
+int  pkh_kv_alloc(int n_layers, int n_kv_heads, int head_dim, int max_seq,
+                  int dtype, pkh_kv_t* kv);
+
+/* Replaces pickle_fast_kv_free (src/pickle_fast.c:1811-1817). */
+void pkh_kv_free(pkh_kv_t* kv);
+
+/* Copy n_pos cache rows of one layer between host and device (dir 0:
+ * device -> host, 1: host -> device).  Host rows use the cache's dtype
+ * (fp16 as uint16 bit patterns).  For callers that seed or inspect a
+ * cache; the reference reads kv->k/v directly (src/pickle_fast.h:153). */
+int  pkh_kv_copy_rows(const pkh_kv_t* kv, int which_v, int layer, int pos0,
+                      int n_pos, void* host, int dir);
+
+/* ------------------------------------------------------------------ */
+/* Device RoPE table                                                  */
+/* ------------------------------------------------------------------ */
+
+/* Device copy of the fast state's sin/cos tables (src/pickle_fast.h:90-95):
+ * [max_seq][half] each, half = min(head_dim / 2, 64). */
+typedef struct {
+    int    max_seq;
+    int    half;
+    int    filled_upto;      /* rows [0, filled_upto) are on the device */
+    float* sin;              /* device */
+    float* cos;              /* device */
+    int    device;
+} pkh_rope_t;
+
+int  pkh_rope_alloc(int max_seq, int half, pkh_rope_t* rope);
+void pkh_rope_free(pkh_rope_t* rope);
+
+/* Upload host rows [rope->filled_upto, filled_upto) of the tables that
+ * pickle_fast_state_extend_rope fills (src/pickle_fast.c:1772-1788); call it
+ * with state->rope_sin, state->rope_cos, state->rope_filled_upto after each
+ * extension.  Rows already on the device are not sent again. */
+int  pkh_rope_upload(pkh_rope_t* rope, const float* sin_tab,
+                     const float* cos_tab, int filled_upto);
+
+/* Host-side table fill with the reference's formulas (src/pickle_fast.c:
+ * 1638-1640 and 1779-1786), for callers that have no pickle_fast_state_t:
+ * inv_freq[i] = 1 / theta^((2i)/head_dim); rows p of sin/cos for
+ * p in [p_begin, p_last] with angle = inv_freq[i] * (float)p. */
+void pkh_rope_host_tables(int head_dim, float theta, int p_begin, int p_last,
+                          float* inv_freq, float* sin_tab, float* cos_tab);
+
+/* ------------------------------------------------------------------ */
+/* Decode: one token of one sequence on one layer                    */
+/* ------------------------------------------------------------------ */
+
+/* Replaces src/pickle_fast.c:1910-2094 for kv != NULL: rotate q and k with
+ * table row pos, write (k_rot, v) into cache row pos of `layer`, attend all
+ * n_heads query heads over rows [0, pos], write ao.  Host pointers; blocks
+ * until ao is written.  pos >= kv->max_seq or pos >= rope->filled_upto
+ * returns PKH_ERR_RANGE before any device work (src/pickle_fast.c:1885). */
+int pkh_attn_decode(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer,
+                    int pos, int n_heads, const float* q, const float* k,
+                    const float* v, float* ao);
+
+/* Same with device pointers, enqueued on `stream`. */
+int pkh_attn_decode_async(const pkh_kv_t* kv, const pkh_rope_t* rope,
+                          int layer, int pos, int n_heads, const float* d_q,
+                          const float* d_k, const float* d_v, float* d_ao,
+                          void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Causal prefill: n_tokens consecutive tokens of one sequence        */
+/* ------------------------------------------------------------------ */
+
+/* Replaces the token loop of src/pickle_fast.c:1881-1898 for the attention
+ * block: row i of q [n][H][D], k/v [n][HK][D] is the token at pos0 + i; its
+ * rotated k and v are written into cache rows pos0 + i and it attends rows
+ * [0, pos0 + i].  Q.K^T and P.V run on MFMA with fp16 operands and fp32
+ * accumulation; softmax is fp32.  Host pointers; blocks until done. */
+int pkh_attn_prefill(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer,
+                     int pos0, int n_tokens, int n_heads, const float* q,
+                     const float* k, const float* v, float* ao);
+
+int pkh_attn_prefill_async(const pkh_kv_t* kv, const pkh_rope_t* rope,
+                           int layer, int pos0, int n_tokens, int n_heads,
+                           const float* d_q, const float* d_k,
+                           const float* d_v, float* d_ao, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Ragged multi-sequence decode                                       */
+/* ------------------------------------------------------------------ */
+
+/* Several sequences' caches in one allocation: sequence s owns slots
+ * [slot0[s], slot0[s] + max_seq[s]) of every layer, each slot one
+ * [n_kv_heads][head_dim] row.  No counterpart in the reference, which keeps
+ * one sequence per pickle_fast_kv_t (src/pickle_fast.h:140-157). */
+typedef struct {
+    int      n_layers;
+    int      n_kv_heads;
+    int      head_dim;
+    int      n_seqs;
+    int      dtype;
+    int      device;
+    size_t   layer_stride;   /* elements per layer (all slots) */
+    int64_t* slot0;          /* host [n_seqs + 1], prefix sum of max_seq */
+    int*     max_seq;        /* host [n_seqs] */
+    void*    k;              /* device */
+    void*    v;              /* device */
+    void*    d_slot0;        /* device copy of slot0 */
+} pkh_kv_batch_t;
+
+int  pkh_kv_batch_alloc(int n_layers, int n_kv_heads, int head_dim,
+                        int n_seqs, const int* max_seq, int dtype,
+                        pkh_kv_batch_t* kvb);
+void pkh_kv_batch_free(pkh_kv_batch_t* kvb);
+
+/* A decode plan: the positions of the next token of every sequence and the
+ * split of each sequence's context into work items.  Build it once per step
+ * (positions change every step); it is reused by every layer of the step. */
+typedef struct pkh_plan pkh_plan_t;
+
+int  pkh_plan_create(const pkh_kv_batch_t* kvb, const int* pos, int n_heads,
+                     pkh_plan_t** plan);
+void pkh_plan_free(pkh_plan_t* plan);
+
+/* One decode step of every sequence on one layer: q [n_seqs][H][D],
+ * k/v [n_seqs][HK][D], ao [n_seqs][H][D], device pointers. */
+int pkh_attn_decode_batch_async(const pkh_kv_batch_t* kvb,
+                                const pkh_rope_t* rope, const pkh_plan_t* plan,
+                                int layer, const float* d_q, const float* d_k,
+                                const float* d_v, float* d_ao, void* stream);
+
+/* Copy n_pos rows of sequence `seq` of one layer between host and device
+ * (dir 0: device -> host, 1: host -> device), in the cache's dtype. */
+int pkh_kv_batch_copy_rows(const pkh_kv_batch_t* kvb, int which_v, int layer,
+                           int seq, int pos0, int n_pos, void* host, int dir);
+
+/* ------------------------------------------------------------------ */
+/* Tuning                                                             */
+/* ------------------------------------------------------------------ */
+
+/* Decode split size: positions per work item (0 = automatic).  Values are
+ * rounded up to the kernel's tile.  Returns the previous setting. */
+int pkh_tune_decode_chunk(int positions);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PKH_ATTN_H */

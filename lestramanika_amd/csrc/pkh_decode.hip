@@ -1,0 +1,582 @@
+// pkh_decode.hip -- split-K flash-decode for gfx950 (CDNA4).
+//
+// Replaces src/pickle_fast.c:1910-2094 (RoPE apply, KV append, attention of
+// one new token over rows [0, pos]) and its multi-sequence generalisation.
+//
+// Work decomposition.  A work item is (sequence, chunk of `chunk` context
+// rows, KV head g).  One workgroup of WAVES wave64s takes one item, so every
+// K/V row it streams from HBM is read once and used for all G = H/HK query
+// heads of the group (the reference re-reads it G times, one OpenMP thread
+// per query head).
+//
+// Register tiling.  A row of D elements is spread over LPP = D/F lanes, F
+// elements per lane, loaded with 16-byte global loads (fp32: 4 elements,
+// fp16: 8) at stride EPL*LPP, so a wave reads PPW = 64/LPP whole rows per
+// tile with fully coalesced 128-bit accesses.  Scores are lane-partial dot
+// products reduced over the LPP lanes of a row with DPP (quad_perm,
+// row_half_mirror, row_mirror).  There is no LDS staging of K/V: each tile is
+// consumed by the wave that loaded it, straight from VGPRs, while the next
+// tile's loads are in flight.
+//
+// Softmax.  Queries are pre-scaled by log2(e)/sqrt(D), so scores are in log2
+// units and exponentials are v_exp_f32.  Each row group keeps its own running
+// max m, running sum l and accumulator; m is raised only when a score exceeds
+// it by more than kTau (a wave-uniform branch that is rarely taken after the
+// first tile), so exp2(s - m) <= 2^kTau and the rescale of the accumulator is
+// skipped on almost every tile.  At the end the row groups of a wave are
+// merged with row_ror DPP and the gfx950 permlane16/32 swaps, waves through
+// LDS, and the workgroup's (m, l, o) is either normalised into the output
+// (single-chunk sequences) or written as a split-K partial for the combine
+// kernel.
+//
+// RoPE and append.  Every workgroup rotates its own G query heads from the
+// host-computed table row `pos` (the same sin/cos bits as the reference's
+// state tables, src/pickle_fast.c:1772-1788).  The workgroup whose chunk
+// contains `pos` rotates the new key for its KV head, stores (k_rot, v) into
+// cache row pos and uses those registers for that row, so no workgroup reads
+// a row another one writes.  The rotation uses the same fused multiply-adds
+// as the reference's build of src/pickle_fast.c:1922-1933.
+
+#include "pkh_internal.h"
+
+#include <cmath>
+#include <cstdio>
+
+namespace pkh {
+namespace {
+
+constexpr float kTau = 8.0f;   // lazy-rescale threshold (log2 units)
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+
+template <typename KT> struct Elt;
+template <> struct Elt<float>    { static constexpr int EPL = 4; };
+template <> struct Elt<_Float16> { static constexpr int EPL = 8; };
+
+template <int D, int G, typename KT>
+struct Shape {
+    static constexpr int EPL = Elt<KT>::EPL;       // elements per 16-byte load
+    static constexpr int F   = (G >= 8) ? 8 : 16;  // elements per lane per row
+    static constexpr int LPP = D / F;              // lanes per row
+    static constexpr int PPW = 64 / LPP;           // rows per wave tile
+    static constexpr int NLD = F / EPL;            // loads per lane per row
+    static constexpr int S   = EPL * LPP;          // element stride between a lane's loads
+    static_assert(D % F == 0 && LPP >= 1 && LPP <= 16, "row split");
+    static_assert(F % EPL == 0, "whole loads per lane");
+};
+
+// ---- cross-lane helpers -----------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the LPP lanes of a row group (aligned, LPP <= 16); every lane of
+// the group receives the sum.
+template <int LPP>
+__device__ __forceinline__ float group_sum(float x) {
+    if constexpr (LPP >= 2)  x += dpp<0xB1>(x);    // quad_perm [1,0,3,2]
+    if constexpr (LPP >= 4)  x += dpp<0x4E>(x);    // quad_perm [2,3,0,1]
+    if constexpr (LPP >= 8)  x += dpp<0x141>(x);   // row_half_mirror
+    if constexpr (LPP >= 16) x += dpp<0x140>(x);   // row_mirror
+    return x;
+}
+
+// Reduce over the 64/LPP row groups of a wave (lanes with equal lane % LPP);
+// every lane receives the result.  Rotations inside a 16-lane row, then the
+// gfx950 row swaps across rows.
+template <int LPP, bool IS_MAX>
+__device__ __forceinline__ float across_groups(float x) {
+    auto op = [](float a, float b) { return IS_MAX ? fmaxf(a, b) : a + b; };
+    if constexpr (LPP <= 1) x = op(x, dpp<0x121>(x));   // row_ror:1
+    if constexpr (LPP <= 2) x = op(x, dpp<0x122>(x));   // row_ror:2
+    if constexpr (LPP <= 4) x = op(x, dpp<0x124>(x));   // row_ror:4
+    if constexpr (LPP <= 8) x = op(x, dpp<0x128>(x));   // row_ror:8
+    {
+        unsigned u = __float_as_uint(x);
+        auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        x = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    {
+        unsigned u = __float_as_uint(x);
+        auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        x = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    }
+    return x;
+}
+
+// ---- element access ---------------------------------------------------
+
+template <typename KT, int NLD>
+__device__ __forceinline__ void unpack(const uint4 (&r)[NLD], float (&f)[NLD * Elt<KT>::EPL]) {
+    if constexpr (sizeof(KT) == 4) {
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            f[4 * i + 0] = __uint_as_float(r[i].x);
+            f[4 * i + 1] = __uint_as_float(r[i].y);
+            f[4 * i + 2] = __uint_as_float(r[i].z);
+            f[4 * i + 3] = __uint_as_float(r[i].w);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            half8_t h = __builtin_bit_cast(half8_t, r[i]);
+#pragma unroll
+            for (int c = 0; c < 8; c++) f[8 * i + c] = (float)h[c];
+        }
+    }
+}
+
+template <typename KT, int NLD, int EPL, int S>
+__device__ __forceinline__ void load_row(uint4 (&r)[NLD], const KT* row, int j) {
+#pragma unroll
+    for (int i = 0; i < NLD; i++)
+        r[i] = *reinterpret_cast<const uint4*>(row + EPL * j + S * i);
+}
+
+// Rotate EPL consecutive elements starting at element b of one head vector x
+// (fp32, global) by table row (sn, cs); half = rotation half-width.  Element
+// i < half becomes fma(c, x[i], -(s*x[i+half])) and element i + half becomes
+// fma(s, x[i], c*x[i+half]): the evaluation of src/pickle_fast.c:1922-1933
+// in the reference's default FMA build, so rotated values match it bit for bit.
+template <int EPL>
+__device__ __forceinline__ void rope_block(float (&out)[EPL], const float* x, int b, int half,
+                                           const float* sn, const float* cs) {
+    if (b < half) {
+#pragma unroll
+        for (int c = 0; c < EPL; c++) {
+            const float a = x[b + c], bb = x[b + c + half];
+            const float co = cs[b + c], si = sn[b + c];
+            out[c] = __builtin_fmaf(co, a, -__fmul_rn(si, bb));
+        }
+    } else if (b < 2 * half) {
+#pragma unroll
+        for (int c = 0; c < EPL; c++) {
+            const float a = x[b + c - half], bb = x[b + c];
+            const float co = cs[b + c - half], si = sn[b + c - half];
+            out[c] = __builtin_fmaf(si, a, __fmul_rn(co, bb));
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < EPL; c++) out[c] = x[b + c];
+    }
+}
+
+template <typename KT>
+__device__ __forceinline__ KT to_kt(float x) { return (KT)x; }
+
+// ---- split kernel -------------------------------------------------------
+
+struct SplitParams {
+    const void* k_layer;
+    const void* v_layer;
+    const float* q;
+    const float* k_new;
+    const float* v_new;
+    float* out;
+    float* part_o;            // [total_chunks][H][D]
+    float* part_ml;           // [total_chunks][H][2]
+    const float* rope_sin;
+    const float* rope_cos;
+    const long long* seq_slot0;
+    const int* seq_pos;
+    const int* chunk_start;
+    long long slot0;
+    int pos;
+    int n_seqs;
+    int H, HK, half, chunk;
+    float qscale;
+};
+
+template <int D, int G, typename KT, int WAVES, bool RAGGED>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_split(SplitParams P) {
+    using SH = Shape<D, G, KT>;
+    constexpr int EPL = SH::EPL, F = SH::F, LPP = SH::LPP, PPW = SH::PPW,
+                  NLD = SH::NLD, S = SH::S;
+
+    __shared__ float red_o[WAVES][G][D];
+    __shared__ float red_m[WAVES][G];
+    __shared__ float red_l[WAVES][G];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int j = lane % LPP;        // slot of this lane inside its row group
+    const int grp = lane / LPP;      // row of the tile handled by this lane
+    const int g = blockIdx.y;        // KV head
+    const int H = P.H, HK = P.HK, half = P.half;
+
+    int seq, c, pos, n_chunks, gchunk;
+    long long slot0;
+    if constexpr (RAGGED) {
+        gchunk = blockIdx.x;
+        int lo = 0, hi = P.n_seqs;   // largest s with chunk_start[s] <= gchunk
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (P.chunk_start[mid] <= gchunk) lo = mid; else hi = mid;
+        }
+        seq = lo;
+        c = gchunk - P.chunk_start[seq];
+        n_chunks = P.chunk_start[seq + 1] - P.chunk_start[seq];
+        pos = P.seq_pos[seq];
+        slot0 = P.seq_slot0[seq];
+    } else {
+        seq = 0;
+        c = blockIdx.x;
+        gchunk = c;
+        n_chunks = gridDim.x;
+        pos = P.pos;
+        slot0 = P.slot0;
+    }
+    const int attend_n = pos + 1;
+    const int p_begin = c * P.chunk;
+    const int p_end = min(p_begin + P.chunk, attend_n);
+    const int n_tiles = (p_end - p_begin + PPW - 1) / PPW;
+
+    // Buffer resources over rows [0, p_end) of this sequence's KV head g:
+    // loads past p_end return zeros, so partial tiles need no predicate.
+    const size_t row_elems = (size_t)HK * D;
+    const unsigned row_bytes = (unsigned)(row_elems * sizeof(KT));
+    KT* kbase = const_cast<KT*>(reinterpret_cast<const KT*>(P.k_layer)) + (size_t)slot0 * row_elems + (size_t)g * D;
+    KT* vbase = const_cast<KT*>(reinterpret_cast<const KT*>(P.v_layer)) + (size_t)slot0 * row_elems + (size_t)g * D;
+    const int extent = (int)((unsigned)p_end * row_bytes - (unsigned)(g * D * sizeof(KT)));
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(kbase, (short)0, extent, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(vbase, (short)0, extent, 0x00020000);
+    const float* sn = P.rope_sin + (size_t)pos * half;
+    const float* cs = P.rope_cos + (size_t)pos * half;
+
+    // Rotated, pre-scaled queries of the G heads of this KV head.
+    float qr[G][F];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        const float* qh = P.q + ((size_t)seq * H + (size_t)g * G + h) * D;
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            float blk[EPL];
+            rope_block<EPL>(blk, qh, EPL * j + S * i, half, sn, cs);
+#pragma unroll
+            for (int e = 0; e < EPL; e++) qr[h][EPL * i + e] = blk[e] * P.qscale;
+        }
+    }
+
+    float m[G], l[G], acc[G][F];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < F; e++) acc[h][e] = 0.0f;
+    }
+
+    // Online-softmax update with one row per lane group.
+    auto consume = [&](const float (&kf)[F], const float (&vf)[F], bool valid) {
+        float s[G];
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            float d0 = 0.0f;
+#pragma unroll
+            for (int e = 0; e < F; e++) d0 = fmaf(qr[h][e], kf[e], d0);
+            s[h] = group_sum<LPP>(d0);
+            if (!valid) s[h] = -INFINITY;
+        }
+        bool need = false;
+#pragma unroll
+        for (int h = 0; h < G; h++) need |= s[h] > m[h] + kTau;
+        if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                const bool nh = s[h] > m[h] + kTau;
+                const float mn = nh ? s[h] : m[h];
+                const float alpha = nh ? __builtin_amdgcn_exp2f(m[h] - mn) : 1.0f;
+                l[h] *= alpha;
+#pragma unroll
+                for (int e = 0; e < F; e++) acc[h][e] *= alpha;
+                m[h] = mn;
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const float pr = valid ? __builtin_amdgcn_exp2f(s[h] - m[h]) : 0.0f;
+            l[h] += pr;
+#pragma unroll
+            for (int e = 0; e < F; e++) acc[h][e] = fmaf(pr, vf[e], acc[h][e]);
+        }
+    };
+
+    const unsigned lane_off = (unsigned)(EPL * j * sizeof(KT));
+    auto issue = [&](int t, uint4 (&kr)[NLD], uint4 (&vr)[NLD]) {
+        const unsigned off = (unsigned)(p_begin + t * PPW + grp) * row_bytes + lane_off;
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                        krs, off + (unsigned)(S * i * sizeof(KT)), 0, 0));
+            vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                        vrs, off + (unsigned)(S * i * sizeof(KT)), 0, 0));
+        }
+    };
+    auto use = [&](int t, const uint4 (&kr)[NLD], const uint4 (&vr)[NLD]) {
+        const int p = p_begin + t * PPW + grp;
+        float kf[F], vf[F];
+        unpack<KT, NLD>(kr, kf);
+        unpack<KT, NLD>(vr, vf);
+        consume(kf, vf, p < p_end && p != pos);
+    };
+
+    // Main loop: this wave's tiles t = wave, wave + WAVES, ...; the next
+    // tile's loads are issued before the current one is consumed.
+    {
+        uint4 ka[NLD], va[NLD], kb[NLD], vb[NLD];  // current tile, next tile
+        int t = wave;
+        if (t < n_tiles) issue(t, ka, va);
+        while (t < n_tiles) {
+            if (t + WAVES < n_tiles) issue(t + WAVES, kb, vb);
+            use(t, ka, va);
+            t += WAVES;
+#pragma unroll
+            for (int i = 0; i < NLD; i++) { ka[i] = kb[i]; va[i] = vb[i]; }
+        }
+    }
+
+    // The new row: rotate k for KV head g, round to the cache type, store
+    // (k_rot, v) into row pos, and fold it into the owning lane group.
+    if (pos >= p_begin && pos < p_end) {
+        const int r = pos - p_begin;
+        if (wave == (r / PPW) % WAVES) {
+            const bool mine = grp == r % PPW;
+            float kf[F], vf[F];
+            const float* kh = P.k_new + ((size_t)seq * HK + g) * D;
+            const float* vh = P.v_new + ((size_t)seq * HK + g) * D;
+            KT* kdst = kbase + (size_t)pos * row_elems;
+            KT* vdst = vbase + (size_t)pos * row_elems;
+#pragma unroll
+            for (int i = 0; i < NLD; i++) {
+                const int b = EPL * j + S * i;
+                float blk[EPL];
+                rope_block<EPL>(blk, kh, b, half, sn, cs);
+#pragma unroll
+                for (int e = 0; e < EPL; e++) {
+                    const KT kq = to_kt<KT>(blk[e]);
+                    const KT vq = to_kt<KT>(vh[b + e]);
+                    if (mine) {
+                        kdst[b + e] = kq;
+                        vdst[b + e] = vq;
+                    }
+                    kf[EPL * i + e] = (float)kq;
+                    vf[EPL * i + e] = (float)vq;
+                }
+            }
+            consume(kf, vf, mine);
+        }
+    }
+
+    // Merge the row groups of this wave.
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        const float M = across_groups<LPP, true>(m[h]);
+        const float f = (m[h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[h] - M);
+        const float lh = across_groups<LPP, false>(l[h] * f);
+#pragma unroll
+        for (int e = 0; e < F; e++) acc[h][e] = across_groups<LPP, false>(acc[h][e] * f);
+        if (grp == 0) {
+#pragma unroll
+            for (int i = 0; i < NLD; i++)
+#pragma unroll
+                for (int e = 0; e < EPL; e++)
+                    red_o[wave][h][EPL * j + S * i + e] = acc[h][EPL * i + e];
+        }
+        if (lane == 0) { red_m[wave][h] = M; red_l[wave][h] = lh; }
+    }
+    __syncthreads();
+
+    // Merge the waves and write the work item's result.
+    for (int idx = threadIdx.x; idx < G * D; idx += 64 * WAVES) {
+        const int h = idx / D, d = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < WAVES; w++) M = fmaxf(M, red_m[w][h]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WAVES; w++) {
+            const float mw = red_m[w][h];
+            const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            L = fmaf(red_l[w][h], f, L);
+            O = fmaf(red_o[w][h][d], f, O);
+        }
+        const int head = g * G + h;
+        if (n_chunks == 1) {
+            P.out[((size_t)seq * H + head) * D + d] = O / L;
+        } else {
+            P.part_o[((size_t)gchunk * H + head) * D + d] = O;
+            if (d == 0) {
+                P.part_ml[((size_t)gchunk * H + head) * 2 + 0] = M;
+                P.part_ml[((size_t)gchunk * H + head) * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// ---- combine kernel -----------------------------------------------------
+
+template <int D>
+__global__ __launch_bounds__(64) void decode_combine(const float* __restrict__ part_o,
+                                                     const float* __restrict__ part_ml,
+                                                     const int* __restrict__ chunk_start,
+                                                     int single_chunks, int H,
+                                                     float* __restrict__ out) {
+    constexpr int PER = (D + 63) / 64;
+    const int head = blockIdx.x, seq = blockIdx.y;
+    const int cb = chunk_start ? chunk_start[seq] : 0;
+    const int ce = chunk_start ? chunk_start[seq + 1] : single_chunks;
+    if (ce - cb <= 1) return;   // single-chunk sequences were finished by the split kernel
+    float M = -INFINITY;
+    for (int c = cb; c < ce; c++) M = fmaxf(M, part_ml[((size_t)c * H + head) * 2]);
+    float L = 0.0f, O[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) O[i] = 0.0f;
+    for (int c = cb; c < ce; c++) {
+        const size_t base = (size_t)c * H + head;
+        const float f = __builtin_amdgcn_exp2f(part_ml[base * 2] - M);
+        L = fmaf(part_ml[base * 2 + 1], f, L);
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int d = threadIdx.x + 64 * i;
+            if (d < D) O[i] = fmaf(part_o[base * D + d], f, O[i]);
+        }
+    }
+    const float inv = 1.0f / L;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int d = threadIdx.x + 64 * i;
+        if (d < D) out[((size_t)seq * H + head) * D + d] = O[i] * inv;
+    }
+}
+
+// ---- dispatch -------------------------------------------------------------
+
+constexpr int kWaves = 4;
+
+template <int D, int G, typename KT>
+int launch_typed(const DecodeArgs& a, const SplitParams& P, int total_chunks, hipStream_t st) {
+    dim3 grid(total_chunks, a.n_kv_heads), block(64 * kWaves);
+    const bool ragged = a.d_chunk_start != nullptr;
+    if (ragged)
+        hipLaunchKernelGGL((decode_split<D, G, KT, kWaves, true>), grid, block, 0, st, P);
+    else
+        hipLaunchKernelGGL((decode_split<D, G, KT, kWaves, false>), grid, block, 0, st, P);
+    PKH_HIP(hipGetLastError());
+    if (a.max_chunks > 1) {
+        dim3 cgrid(a.n_heads, a.n_seqs);
+        hipLaunchKernelGGL((decode_combine<D>), cgrid, dim3(64), 0, st, P.part_o, P.part_ml,
+                           a.d_chunk_start, total_chunks, a.n_heads, a.out);
+        PKH_HIP(hipGetLastError());
+    }
+    return PKH_OK;
+}
+
+template <typename KT>
+int launch_kt(const DecodeArgs& a, const SplitParams& P, int tc, hipStream_t st) {
+    const int G = a.n_heads / a.n_kv_heads;
+#define PKH_CASE(DD, GG) \
+    if (a.head_dim == DD && G == GG) return launch_typed<DD, GG, KT>(a, P, tc, st);
+    PKH_CASE(16, 1) PKH_CASE(16, 2) PKH_CASE(16, 4) PKH_CASE(16, 8)
+    PKH_CASE(32, 1) PKH_CASE(32, 2) PKH_CASE(32, 4) PKH_CASE(32, 8)
+    PKH_CASE(64, 1) PKH_CASE(64, 2) PKH_CASE(64, 4) PKH_CASE(64, 8)
+    PKH_CASE(128, 1) PKH_CASE(128, 2) PKH_CASE(128, 4) PKH_CASE(128, 8)
+    PKH_CASE(256, 1) PKH_CASE(256, 2) PKH_CASE(256, 4)
+#undef PKH_CASE
+    return PKH_ERR_ARG;
+}
+
+}  // namespace
+
+bool shape_supported(int head_dim, int group) {
+    const bool g_ok = group == 1 || group == 2 || group == 4 || group == 8;
+    switch (head_dim) {
+        case 16: case 32: case 64: case 128: return g_ok;
+        case 256: return g_ok && group <= 4;
+        default: return false;
+    }
+}
+
+int decode_tile_positions(int head_dim, int group, int dtype) {
+    (void)dtype;
+    const int F = group >= 8 ? 8 : 16;
+    const int lpp = head_dim / F;
+    return (64 / lpp) * kWaves;
+}
+
+static int g_chunk_override = 0;
+
+int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
+                     int n_kv_heads, int max_attend) {
+    const int tile = decode_tile_positions(head_dim, group, dtype);
+    long long chunk;
+    if (g_chunk_override > 0) {
+        chunk = g_chunk_override;
+    } else {
+        // Aim for about 2048 resident waves (8 per CU on 256 CUs) with at
+        // least four tiles per wave, so per-item setup stays small.
+        const long long target_items = 2048 / kWaves;
+        chunk = (total_rows * n_kv_heads + target_items - 1) / target_items;
+        if (chunk < 4LL * tile) chunk = 4LL * tile;
+    }
+    chunk = (chunk + tile - 1) / tile * tile;
+    if (chunk > (long long)max_attend) chunk = ((long long)max_attend + tile - 1) / tile * tile;
+    if (chunk < tile) chunk = tile;
+    return (int)chunk;
+}
+
+int launch_decode(const DecodeArgs& a, hipStream_t st) {
+    const int H = a.n_heads, D = a.head_dim;
+    SplitParams P{};
+    P.k_layer = a.k_layer;
+    P.v_layer = a.v_layer;
+    P.q = a.q;
+    P.k_new = a.k_new;
+    P.v_new = a.v_new;
+    P.out = a.out;
+    P.rope_sin = a.rope_sin;
+    P.rope_cos = a.rope_cos;
+    P.seq_slot0 = a.d_seq_slot0;
+    P.seq_pos = a.d_seq_pos;
+    P.chunk_start = a.d_chunk_start;
+    P.slot0 = a.slot0;
+    P.pos = a.pos;
+    P.n_seqs = a.n_seqs;
+    P.H = H;
+    P.HK = a.n_kv_heads;
+    P.half = a.half;
+    P.chunk = a.chunk;
+    P.qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
+
+    // Buffer-resource offsets are 32-bit: one sequence's rows of a layer
+    // must stay below 2 GiB.
+    const long long elem = a.dtype == PKH_KV_F16 ? 2 : 4;
+    const long long max_rows = a.n_seqs == 1 && !a.d_chunk_start
+                                   ? (long long)a.pos + 1
+                                   : (long long)a.max_chunks * a.chunk;
+    if (max_rows * a.n_kv_heads * D * elem >= (1LL << 31)) return PKH_ERR_ARG;
+
+    const int total_chunks = a.total_chunks;
+    if (a.max_chunks > 1) {
+        const size_t n_o = (size_t)total_chunks * H * D;
+        const size_t n_ml = (size_t)total_chunks * H * 2;
+        void* ws = nullptr;
+        int rc = scratch_get((n_o + n_ml) * sizeof(float), &ws);
+        if (rc != PKH_OK) return rc;
+        P.part_o = reinterpret_cast<float*>(ws);
+        P.part_ml = P.part_o + n_o;
+    }
+    if (a.dtype == PKH_KV_F32) return launch_kt<float>(a, P, total_chunks, st);
+    if (a.dtype == PKH_KV_F16) return launch_kt<_Float16>(a, P, total_chunks, st);
+    return PKH_ERR_ARG;
+}
+
+}  // namespace pkh
+
+extern "C" int pkh_tune_decode_chunk(int positions) {
+    const int prev = pkh::g_chunk_override;
+    pkh::g_chunk_override = positions > 0 ? positions : 0;
+    return prev;
+}

@@ -1,0 +1,90 @@
+// pkh_internal.h -- shared declarations of the HIP attention library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "pkh_attn.h"
+
+namespace pkh {
+
+// Map a HIP error to a PKH_ERR_* code, with one line on stderr naming the call.
+int hip_fail(hipError_t e, const char* what);
+
+#define PKH_HIP(expr)                                                  \
+    do {                                                               \
+        hipError_t pkh_e_ = (expr);                                    \
+        if (pkh_e_ != hipSuccess) return ::pkh::hip_fail(pkh_e_, #expr); \
+    } while (0)
+
+// Per-device grow-only scratch owned by the library (split-K partials).
+int scratch_get(size_t bytes, void** out);
+
+// Per-device grow-only staging buffers for the host-pointer entry points.
+int staging_get(int slot, size_t bytes, void** out);
+
+// Current device of the library.
+int current_device();
+
+// True for the (head_dim, group) pairs the kernels are instantiated for.
+bool shape_supported(int head_dim, int group);
+
+// ---- decode ------------------------------------------------------------
+
+// One decode launch: n_seqs sequences (1 for the single-sequence path),
+// each with its own position and slot base inside one layer's cache.
+struct DecodeArgs {
+    const void* k_layer;      // layer base, element type per dtype
+    const void* v_layer;
+    int dtype;                // PKH_KV_F32 / PKH_KV_F16
+    int head_dim, n_heads, n_kv_heads;
+    int n_seqs;
+    // single sequence (n_seqs == 1 and seq arrays null):
+    int pos;
+    long long slot0;
+    // ragged (device arrays, n_seqs entries; chunk_start has n_seqs + 1):
+    const long long* d_seq_slot0;
+    const int* d_seq_pos;
+    const int* d_chunk_start;
+    int total_chunks;         // sum of chunks over sequences
+    int max_chunks;           // largest per-sequence chunk count
+    int chunk;                // positions per work item
+    const float* q;           // [n_seqs][H][D]
+    const float* k_new;       // [n_seqs][HK][D]
+    const float* v_new;
+    float* out;               // [n_seqs][H][D]
+    const float* rope_sin;    // [max_seq][half]
+    const float* rope_cos;
+    int half;
+};
+
+// Positions per work item for a context of attend_n rows (tile-aligned).
+int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
+                     int n_kv_heads, int max_attend);
+int decode_tile_positions(int head_dim, int group, int dtype);
+
+int launch_decode(const DecodeArgs& a, hipStream_t stream);
+
+// ---- prefill -----------------------------------------------------------
+
+struct PrefillArgs {
+    void* k_layer;            // fp32 or fp16 cache, layer base
+    void* v_layer;
+    int dtype;
+    int head_dim, n_heads, n_kv_heads;
+    int pos0, n_tokens;
+    const float* q;           // [n][H][D]
+    const float* k_new;       // [n][HK][D]
+    const float* v_new;
+    float* out;               // [n][H][D]
+    const float* rope_sin;
+    const float* rope_cos;
+    int half;
+};
+
+bool prefill_supported(int head_dim, int group, int dtype);
+int launch_prefill(const PrefillArgs& a, hipStream_t stream);
+
+}  // namespace pkh

@@ -1,0 +1,128 @@
+"""CPU checks of the C ABI library (lestramanika_amd/libpkh.so).
+
+No kernel runs here: the library is loaded, its exports are checked against
+include/pkh_attn.h, its host-only helpers are compared with the oracle, and
+every argument check that returns before touching the device is exercised.
+"""
+import ctypes
+import hashlib
+import json
+import os
+import re
+
+import numpy as np
+import pytest
+
+import lestramanika_amd as pk
+from oracle import pyoracle as po
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pkh_attn.h")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pkh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = pk.load()
+    names = declared_functions()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(pk._SIGS), "bindings and header disagree"
+    assert b"gfx950" in lib.pkh_version()
+
+
+def test_oracle_library_exports():
+    lib = po.lib()
+    for name in ["pko_rope_inv_freq", "pko_rope_fill", "pko_rope_apply", "pko_attend_f32",
+                 "pko_decode_step_f32", "pko_decode_step_f16", "pko_prefill_f32"]:
+        assert hasattr(lib, name)
+
+
+def test_host_rope_tables_match_oracle_and_reference():
+    lib = pk.load()
+    tabs = json.load(open(os.path.join(GOLDEN, "rope_tables.json")))
+    for key, t in tabs.items():
+        D, theta, n = t["head_dim"], t["theta"], t["n_pos"]
+        half = min(D // 2, 64)
+        inv = np.zeros(half, np.float32)
+        sin = np.zeros((n, half), np.float32)
+        cos = np.zeros((n, half), np.float32)
+        lib.pkh_rope_host_tables(D, theta, 0, n - 1, inv.ctypes.data, sin.ctypes.data,
+                                 cos.ctypes.data)
+        assert hashlib.sha256(inv.tobytes()).hexdigest() == t["inv_freq"], key
+        assert hashlib.sha256(sin.tobytes()).hexdigest() == t["sin"], key
+        assert hashlib.sha256(cos.tobytes()).hexdigest() == t["cos"], key
+        oi, os_, oc = po.rope_tables(D, theta, min(n, 64))
+        assert np.array_equal(inv, oi) and np.array_equal(sin[:64], os_)
+
+
+def _fake_kv(n_layers=2, HK=2, D=64, max_seq=16, dtype=pk.PKH_KV_F32):
+    kv = pk.KV()
+    kv.n_layers, kv.n_kv_heads, kv.head_dim, kv.max_seq = n_layers, HK, D, max_seq
+    kv.k_stride_layer = kv.v_stride_layer = max_seq * HK * D
+    kv.k = kv.v = 0x1000      # never dereferenced: every call below fails its checks first
+    kv.dtype = dtype
+    return kv
+
+
+def _fake_rope(max_seq=16, half=32, filled=16):
+    r = pk.Rope()
+    r.max_seq, r.half, r.filled_upto = max_seq, half, filled
+    r.sin = r.cos = 0x2000
+    return r
+
+
+def test_argument_checks_return_before_device_work():
+    lib = pk.load()
+    kv, rope = _fake_kv(), _fake_rope()
+    dummy = ctypes.c_void_p(0x3000)
+    dec = lambda kv_, rope_, layer, pos, H: lib.pkh_attn_decode(
+        ctypes.byref(kv_) if kv_ is not None else None,
+        ctypes.byref(rope_) if rope_ is not None else None, layer, pos, H,
+        dummy, dummy, dummy, dummy)
+    assert dec(None, rope, 0, 0, 4) == pk.PKH_ERR_ARG
+    assert dec(kv, None, 0, 0, 4) == pk.PKH_ERR_ARG
+    assert dec(kv, rope, 2, 0, 4) == pk.PKH_ERR_RANGE        # layer
+    assert dec(kv, rope, -1, 0, 4) == pk.PKH_ERR_RANGE
+    assert dec(kv, rope, 0, 16, 4) == pk.PKH_ERR_RANGE       # pos >= max_seq
+    assert dec(kv, rope, 0, -1, 4) == pk.PKH_ERR_RANGE
+    assert dec(kv, _fake_rope(filled=5), 0, 5, 4) == pk.PKH_ERR_RANGE   # table not uploaded
+    assert dec(kv, rope, 0, 0, 3) == pk.PKH_ERR_ARG          # H % HK != 0
+    assert dec(kv, rope, 0, 0, 32) == pk.PKH_ERR_ARG         # group 16 unsupported
+    assert dec(kv, _fake_rope(half=16), 0, 0, 4) == pk.PKH_ERR_ARG      # table of another D
+    assert dec(_fake_kv(D=24), _fake_rope(half=12), 0, 0, 4) == pk.PKH_ERR_ARG
+    assert lib.pkh_attn_decode_async(ctypes.byref(kv), ctypes.byref(rope), 0, 0, 4,
+                                     None, dummy, dummy, dummy, None) == pk.PKH_ERR_ARG
+    pf = lambda pos0, n: lib.pkh_attn_prefill(ctypes.byref(kv), ctypes.byref(rope), 0, pos0, n,
+                                              4, dummy, dummy, dummy, dummy)
+    assert pf(0, 0) in (pk.PKH_ERR_ARG,)
+    assert pf(10, 7) in (pk.PKH_ERR_RANGE, pk.PKH_ERR_ARG)
+    k = pk.KV()
+    assert lib.pkh_kv_alloc(0, 2, 64, 16, 0, ctypes.byref(k)) == pk.PKH_ERR_ARG
+    assert lib.pkh_kv_alloc(1, 2, 64, 16, 7, ctypes.byref(k)) == pk.PKH_ERR_ARG
+    assert lib.pkh_kv_alloc(1, 2, 64, 16, 0, None) == pk.PKH_ERR_ARG
+    r = pk.Rope()
+    assert lib.pkh_rope_alloc(16, 65, ctypes.byref(r)) == pk.PKH_ERR_ARG
+    assert lib.pkh_rope_alloc(0, 8, ctypes.byref(r)) == pk.PKH_ERR_ARG
+    b = pk.KVBatch()
+    ms = (ctypes.c_int * 2)(16, 0)
+    assert lib.pkh_kv_batch_alloc(1, 2, 64, 2, ms, 0, ctypes.byref(b)) == pk.PKH_ERR_ARG
+    plan = ctypes.c_void_p()
+    assert lib.pkh_plan_create(None, None, 4, ctypes.byref(plan)) == pk.PKH_ERR_ARG
+    # freeing zeroed structs is a no-op, as for the reference's *_free
+    lib.pkh_kv_free(ctypes.byref(pk.KV()))
+    lib.pkh_rope_free(ctypes.byref(pk.Rope()))
+    lib.pkh_kv_batch_free(ctypes.byref(pk.KVBatch()))
+    lib.pkh_plan_free(None)
+
+
+def test_tuning_hook_round_trips():
+    lib = pk.load()
+    prev = lib.pkh_tune_decode_chunk(512)
+    assert lib.pkh_tune_decode_chunk(prev) == 512

@@ -1,0 +1,207 @@
+"""GPU parity of the decode path (pkh_attn_decode*) against the oracle and the
+reference's own outputs, through the C ABI.
+
+Tolerances (written here, as stated for the path): max-abs 1e-4 for an fp32
+KV cache, 2e-3 for fp16.  The appended cache row is compared bit for bit.
+"""
+import ctypes
+import glob
+import os
+
+import numpy as np
+import pytest
+
+import lestramanika_amd as pk
+from oracle import pyoracle as po
+from pkh_util import DeviceKV, DeviceRope, decode_host, log, maxerr, normal
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+TOL_F16 = 2e-3
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _run_case(H, HK, D, pos, theta, seed, dtype=pk.PKH_KV_F32, layer=0, n_layers=1,
+              max_seq=None, threads=16):
+    max_seq = max_seq or pos + 1
+    kc = normal(seed, (max_seq, HK, D))
+    vc = normal(seed + 1, (max_seq, HK, D))
+    q = normal(seed + 2, (H, D))
+    k = normal(seed + 3, (HK, D))
+    v = normal(seed + 4, (HK, D))
+    kv = DeviceKV(n_layers, HK, D, max_seq, dtype)
+    rope = DeviceRope(D, theta, pos + 1, max_seq=max_seq)
+    try:
+        if dtype == pk.PKH_KV_F16:
+            kc16, vc16 = po.f32_to_f16_bits(kc), po.f32_to_f16_bits(vc)
+            kv.write(0, layer, 0, kc16[:pos])
+            kv.write(1, layer, 0, vc16[:pos])
+            ao = decode_host(kv, rope, layer, pos, q, k, v)
+            k16, v16 = kc16[:pos + 1].copy(), vc16[:pos + 1].copy()
+            ref = po.decode_step_f16(k16, v16, pos, q, k, v, rope.sin, rope.cos, threads)
+            row_k, row_v = kv.read(0, layer, pos, 1)[0], kv.read(1, layer, pos, 1)[0]
+            assert np.array_equal(row_k, k16[pos]) and np.array_equal(row_v, v16[pos])
+        else:
+            kv.write(0, layer, 0, kc[:pos])
+            kv.write(1, layer, 0, vc[:pos])
+            ao = decode_host(kv, rope, layer, pos, q, k, v)
+            kr_c, vr_c = kc[:pos + 1].copy(), vc[:pos + 1].copy()
+            ref, _, k_rot = po.decode_step(kr_c, vr_c, pos, q, k, v, rope.sin, rope.cos, threads)
+            row_k, row_v = kv.read(0, layer, pos, 1)[0], kv.read(1, layer, pos, 1)[0]
+            assert np.array_equal(row_k, k_rot), "appended k row differs from the oracle"
+            assert np.array_equal(row_v, v), "appended v row differs"
+        return ao, ref, kv, rope
+    except BaseException:
+        kv.free()
+        rope.free()
+        raise
+
+
+def _check(H, HK, D, pos, theta, seed, dtype=pk.PKH_KV_F32, **kw):
+    log(f"decode H{H} HK{HK} D{D} pos{pos} theta{theta:g} dtype{dtype} seed{seed} {kw}")
+    ao, ref, kv, rope = _run_case(H, HK, D, pos, theta, seed, dtype, **kw)
+    kv.free()
+    rope.free()
+    err = maxerr(ao, ref)
+    log(f"  max-abs err {err:.3e}")
+    assert err <= (TOL_F16 if dtype == pk.PKH_KV_F16 else TOL_F32)
+    return err
+
+
+PROBES = [p for p in sorted(glob.glob(os.path.join(GOLDEN, "attn_probe_*.npz")))]
+
+
+@pytest.mark.parametrize("path", PROBES, ids=[os.path.basename(p)[11:-4] for p in PROBES])
+def test_decode_matches_reference_outputs(path):
+    """GPU decode against the compiled reference's own ao on the probe inputs."""
+    z = np.load(path)
+    H, HK, D, pos = (int(x) for x in z["shape"])
+    if H % HK or D % 16 or D not in (16, 32, 64, 128, 256):
+        pytest.skip("shape outside the GPU path's support (returns PKH_ERR_ARG)")
+    log(f"probe {os.path.basename(path)}")
+    kv = DeviceKV(1, HK, D, pos + 1)
+    rope = DeviceRope(D, float(z["theta"]), pos + 1)
+    try:
+        if pos:
+            kv.write(0, 0, 0, z["cache_k"])
+            kv.write(1, 0, 0, z["cache_v"])
+        ao = decode_host(kv, rope, 0, pos, z["q"], z["k"], z["v"])
+        assert np.array_equal(kv.read(0, 0, pos, 1)[0], z["row_k"])
+        assert np.array_equal(kv.read(1, 0, pos, 1)[0], z["row_v"])
+        err = maxerr(ao, z["ao"])
+        log(f"  max-abs err vs reference {err:.3e}")
+        assert err <= TOL_F32
+    finally:
+        kv.free()
+        rope.free()
+
+
+def test_decode_unsupported_shapes_are_rejected():
+    lib = pk.load()
+    kv = DeviceKV(1, 4, 16, 8)
+    rope = DeviceRope(16, 1e4, 8)
+    try:
+        q = np.zeros((6, 16), np.float32)
+        k = np.zeros((4, 16), np.float32)
+        ao = np.zeros_like(q)
+        rc = lib.pkh_attn_decode(kv.ref, rope.ref, 0, 3, 6, q.ctypes.data, k.ctypes.data,
+                                 k.ctypes.data, ao.ctypes.data)
+        assert rc == pk.PKH_ERR_ARG
+        rc = lib.pkh_attn_decode(kv.ref, rope.ref, 0, 8, 8, q.ctypes.data, k.ctypes.data,
+                                 k.ctypes.data, ao.ctypes.data)
+        assert rc == pk.PKH_ERR_RANGE
+    finally:
+        kv.free()
+        rope.free()
+
+
+def test_decode_tinyllama_shape_ctx2048():
+    """TinyLlama-1.1B shape: H32 HK4 D64, 2048 cached rows, theta 1e4, seed 2."""
+    _check(32, 4, 64, 2048, 1e4, 2)
+
+
+def test_decode_llama3_8b_shape_ctx8192():
+    """Llama-3-8B shape: H32 HK8 D128, 8192 cached rows, theta 5e5, seed 3,
+    on layer 1 of a two-layer cache."""
+    _check(32, 8, 128, 8192, 5e5, 3, layer=1, n_layers=2)
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_decode_shape_sweep(D, G):
+    if D == 256 and G == 8:
+        pytest.skip("head_dim 256 supports groups up to 4")
+    HK = 2
+    for pos in (0, 1, 63, 130, 1031):
+        _check(G * HK, HK, D, pos, 1e4, 100 + D + G + pos)
+
+
+@pytest.mark.parametrize("D,G", [(16, 2), (64, 8), (128, 4), (128, 8), (256, 1)])
+def test_decode_fp16_kv(D, G):
+    for pos in (0, 5, 700, 4100):
+        _check(G * 2, 2, D, pos, 5e5, 200 + D + pos, dtype=pk.PKH_KV_F16)
+
+
+def test_decode_chunking_is_invisible():
+    """Different split-K chunk sizes (one chunk, many chunks) agree within
+    tolerance, and a repeated call is bit-identical."""
+    lib = pk.load()
+    H, HK, D, pos = 32, 8, 128, 3000
+    outs = []
+    try:
+        for chunk in (0, 32, 96, 512, 4096):
+            lib.pkh_tune_decode_chunk(chunk)
+            ao, ref, kv, rope = _run_case(H, HK, D, pos, 5e5, 9)
+            ao2 = decode_host(kv, rope, 0, pos, normal(11, (H, D)), normal(12, (HK, D)),
+                              normal(13, (HK, D)))
+            ao3 = decode_host(kv, rope, 0, pos, normal(11, (H, D)), normal(12, (HK, D)),
+                              normal(13, (HK, D)))
+            kv.free()
+            rope.free()
+            assert np.array_equal(ao2, ao3)
+            err = maxerr(ao, ref)
+            log(f"chunk {chunk}: max-abs err {err:.3e}")
+            assert err <= TOL_F32
+            outs.append(ao)
+    finally:
+        lib.pkh_tune_decode_chunk(0)
+    for o in outs[1:]:
+        assert maxerr(o, outs[0]) <= 2 * TOL_F32
+
+
+def test_decode_other_layers_untouched():
+    H, HK, D, pos = 8, 2, 64, 100
+    ao, ref, kv, rope = _run_case(H, HK, D, pos, 1e4, 21, layer=1, n_layers=3, max_seq=128)
+    try:
+        assert maxerr(ao, ref) <= TOL_F32
+        for L in (0, 2):
+            assert not kv.read(0, L, 0, 128).any() and not kv.read(1, L, 0, 128).any()
+        # rows past pos in the written layer are still zero
+        assert not kv.read(0, 1, pos + 1, 128 - pos - 1).any()
+    finally:
+        kv.free()
+        rope.free()
+
+
+def test_decode_async_on_torch_stream_matches_host_entry():
+    import torch
+    lib = pk.load()
+    H, HK, D, pos = 32, 8, 128, 5000
+    ao, ref, kv, rope = _run_case(H, HK, D, pos, 5e5, 31)
+    try:
+        dev = torch.device("cuda")
+        q = torch.from_numpy(normal(33, (H, D))).to(dev)
+        k = torch.from_numpy(normal(34, (HK, D))).to(dev)
+        v = torch.from_numpy(normal(35, (HK, D))).to(dev)
+        out = torch.empty((H, D), dtype=torch.float32, device=dev)
+        s = torch.cuda.current_stream()
+        rc = lib.pkh_attn_decode_async(kv.ref, rope.ref, 0, pos, H, q.data_ptr(), k.data_ptr(),
+                                       v.data_ptr(), out.data_ptr(), ctypes.c_void_p(s.cuda_stream))
+        assert rc == 0
+        torch.cuda.synchronize()
+        host = decode_host(kv, rope, 0, pos, q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy())
+        assert np.array_equal(out.cpu().numpy(), host)
+    finally:
+        kv.free()
+        rope.free()
