@@ -75,8 +75,8 @@ def cpu_baseline_decode(K, V, q, k, v, cfg, layers, threads):
     from oracle import pyoracle as po
     H, HK, D, ctx = cfg["H"], cfg["HK"], cfg["D"], cfg["ctx"]
     _, sin, cos = po.rope_tables(D, cfg["theta"], ctx + 1)
-    host = [(K[L].cpu().numpy(), V[L].cpu().numpy(), q[L].cpu().numpy(), k[L].cpu().numpy(),
-             v[L].cpu().numpy()) for L in range(layers)]
+    host = [(K[L].contiguous().cpu().numpy(), V[L].contiguous().cpu().numpy(),
+             q[L].cpu().numpy(), k[L].cpu().numpy(), v[L].cpu().numpy()) for L in range(layers)]
     kc, vc, qq, kk, vv = host[0]
     po.decode_step(kc, vc, ctx, qq, kk, vv, sin, cos, threads)     # warm-up
     t0 = time.perf_counter()
@@ -98,23 +98,26 @@ def run_decode(args, cfg):
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(cfg["seed"])
-    log(f"bench: allocating {L} layers x {max_seq} rows x {HK}x{D} fp32 K and V")
-    K = torch.zeros((L, max_seq, HK, D), dtype=torch.float32, device=dev)
-    V = torch.zeros((L, max_seq, HK, D), dtype=torch.float32, device=dev)
+    log(f"bench: allocating {L} layers x {HK} heads x {max_seq} rows x (K {D} | V {D}) fp32")
+    # The cache in the library's default device layout (each layer
+    # [kv_head][pos][K row | V row]); pkh_kv_t is caller-owned, as
+    # pickle_fast_kv_t is, so it can point at torch's buffer.
+    KV = torch.zeros((L, HK, max_seq, 2, D), dtype=torch.float32, device=dev)
     for layer in range(L):
-        K[layer, :ctx].normal_(generator=gen)
-        V[layer, :ctx].normal_(generator=gen)
+        KV[layer, :, :ctx].normal_(generator=gen)
+    K = KV[:, :, :, 0, :].permute(0, 2, 1, 3)       # [L][pos][HK][D] views
+    V = KV[:, :, :, 1, :].permute(0, 2, 1, 3)
     q = torch.randn((L, H, D), generator=gen, device=dev)
     k = torch.randn((L, HK, D), generator=gen, device=dev)
     v = torch.randn((L, HK, D), generator=gen, device=dev)
     ao = torch.zeros((L, H, D), device=dev)
 
-    # The cache struct points at torch's buffers (pkh_kv_t is caller-owned,
-    # as pickle_fast_kv_t is).
     kv = pk.KV()
     kv.n_layers, kv.n_kv_heads, kv.head_dim, kv.max_seq = L, HK, D, max_seq
-    kv.k_stride_layer = kv.v_stride_layer = max_seq * HK * D
-    kv.k, kv.v, kv.dtype, kv.device = K.data_ptr(), V.data_ptr(), pk.PKH_KV_F32, 0
+    kv.k_stride_layer = kv.v_stride_layer = HK * max_seq * 2 * D
+    kv.k, kv.v = KV.data_ptr(), KV.data_ptr() + D * 4
+    kv.dtype, kv.device = pk.PKH_KV_F32, 0
+    kv.stride_pos, kv.stride_head = 2 * D, max_seq * 2 * D
 
     half = min(D // 2, 64)
     sin = np.zeros((max_seq, half), np.float32)
@@ -125,8 +128,6 @@ def run_decode(args, cfg):
     pk.check(lib.pkh_rope_upload(ctypes.byref(rope), sin.ctypes.data, cos.ctypes.data, max_seq),
              "pkh_rope_upload")
 
-    stream = torch.cuda.current_stream()
-    sp = ctypes.c_void_p(stream.cuda_stream)
     kvp, rp = ctypes.byref(kv), ctypes.byref(rope)
     qp = [q[i].data_ptr() for i in range(L)]
     kp = [k[i].data_ptr() for i in range(L)]
@@ -134,39 +135,49 @@ def run_decode(args, cfg):
     op = [ao[i].data_ptr() for i in range(L)]
     call = lib.pkh_attn_decode_async
 
-    def step(events=None):
+    def step(stream):
+        sp = ctypes.c_void_p(stream.cuda_stream)
         for layer in range(L):
-            if events is not None:
-                events[layer][0].record(stream)
             rc = call(kvp, rp, layer, ctx, H, qp[layer], kp[layer], vp[layer], op[layer], sp)
             if rc != 0:
                 raise pk.PkhError(rc, "pkh_attn_decode_async")
-            if events is not None:
-                events[layer][1].record(stream)
 
-    log(f"bench: warmup {args.warmup} steps")
+    stream = torch.cuda.current_stream()
+    log(f"bench: warmup {args.warmup} eager steps")
     for _ in range(args.warmup):
-        step()
+        step(stream)
     torch.cuda.synchronize()
 
-    # Timed region 1: wall time of exactly K back-to-back steps.
-    log(f"bench: timing {args.steps} steps x {L} layers")
-    torch.cuda.synchronize()
+    # Eager launches: one host call per layer (reported beside the graph).
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        step(stream)
+    torch.cuda.synchronize()
+    eager_wall = time.perf_counter() - t0
+
+    # The 32-layer step captured once as a HIP graph and replayed: what a
+    # decode loop runs, without per-kernel host launch cost.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(torch.cuda.current_stream())
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+
+    # Timed region: exactly K replays, bracketed by synchronize, with HIP
+    # events on the replay stream around each replay.
+    log(f"bench: timing {args.steps} graph replays x {L} layers")
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1 in evs:
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-
-    # Timed region 2: the same launches bracketed by HIP events on the launch
-    # stream, for the per-launch kernel duration.
-    evs = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
-            for _ in range(L)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    for s in range(args.steps):
-        step(evs[s])
-    torch.cuda.synchronize()
-    durs = np.array([e0.elapsed_time(e1) for st in evs for e0, e1 in st]) * 1e-3  # s
+    durs = np.array([e0.elapsed_time(e1) for e0, e1 in evs]) * 1e-3 / L   # s per layer-step
 
     s_kv = 4
     bpl = decode_bytes(ctx, H, HK, D, s_kv)
@@ -179,7 +190,8 @@ def run_decode(args, cfg):
     _, osin, ocos = po.rope_tables(D, cfg["theta"], max_seq)
     errs = []
     for layer in sorted({0, L - 1}):
-        ref, _, _ = po.decode_step(K[layer].cpu().numpy(), V[layer].cpu().numpy(), ctx,
+        ref, _, _ = po.decode_step(K[layer].contiguous().cpu().numpy(),
+                                   V[layer].contiguous().cpu().numpy(), ctx,
                                    q[layer].cpu().numpy(), k[layer].cpu().numpy(),
                                    v[layer].cpu().numpy(), osin, ocos, n_threads=16)
         errs.append(float(np.max(np.abs(ao[layer].cpu().numpy() - ref))))
@@ -216,13 +228,14 @@ def run_decode(args, cfg):
                    "context": ctx, "layers": L, "kv_dtype": cfg["kv"],
                    "rope_theta": cfg["theta"], "new_token_pos": ctx},
         "us_per_layer_step": round(wall / n_launch * 1e6, 3),
+        "eager_us_per_layer_step": round(eager_wall / n_launch * 1e6, 3),
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "bytes_per_layer_step": bpl,
         "max_abs_err_vs_oracle": max(errs),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_from_profiles(args.workload),
-                     "kernel_us": round(avg_launch * 1e6, 3)},
+                     "us_per_launch": round(avg_launch * 1e6, 3)},
         "cpu_baseline": cpu,
     }
     return result

@@ -21,8 +21,10 @@
  *   q   [n_heads][head_dim]           ao  [n_heads][head_dim]
  *   k,v [n_kv_heads][head_dim]        (the reference's state->q/k/v/ao,
  *                                      src/pickle_fast.h:107-110)
- *   KV  [layer][pos][kv_head][head_dim], fp32 or fp16, in device memory
- *       (the reference's layout, src/pickle_fast.c:1940-1942)
+ *   KV  layer-major, fp32 or fp16, in device memory; within a layer the
+ *       placement is given by strides (pkh_kv_t), head-major by default, the
+ *       reference's [pos][kv_head][head_dim] (src/pickle_fast.c:1940-1942)
+ *       when described so
  *   query head h reads KV head h * n_kv_heads / n_heads
  *   (src/pickle_fast.c:1963); n_heads must be a multiple of n_kv_heads.
  *
@@ -65,25 +67,37 @@ const char* pkh_version(void);
 /* Device KV cache                                                    */
 /* ------------------------------------------------------------------ */
 
-/* Device-resident mirror of pickle_fast_kv_t (src/pickle_fast.h:145-154):
- * the first eight fields have the reference's names and meaning (strides
- * are in elements); k and v are device pointers of element type dtype. */
+/* Device-resident mirror of pickle_fast_kv_t (src/pickle_fast.h:145-154).
+ * The first eight fields have the reference's names and meaning; k and v are
+ * device pointers of element type dtype, and the placement of element
+ * (layer L, position p, KV head g, dim d) is given by strides in elements:
+ *     k + L*k_stride_layer + g*stride_head + p*stride_pos + d
+ * (v likewise from v + L*v_stride_layer).  pkh_kv_alloc lays each layer out
+ * head-major with a position's K and V rows side by side (stride_pos =
+ * 2*head_dim, stride_head = max_seq*2*head_dim, v = k + head_dim), so a
+ * decode work item streams one contiguous block per KV head.  The
+ * reference's own layout [layer][pos][kv_head][dim] is the strides
+ * stride_pos = n_kv_heads*head_dim, stride_head = head_dim with separate K
+ * and V buffers; the kernels accept either. */
 typedef struct {
     int    n_layers;
     int    n_kv_heads;
     int    head_dim;
     int    max_seq;
-    size_t k_stride_layer;   /* max_seq * n_kv_heads * head_dim */
-    size_t v_stride_layer;
-    void*  k;                /* device [n_layers * k_stride_layer] */
-    void*  v;                /* device [n_layers * v_stride_layer] */
+    size_t k_stride_layer;   /* elements between layers of K */
+    size_t v_stride_layer;   /* elements between layers of V */
+    void*  k;                /* device; for pkh_kv_alloc the allocation base */
+    void*  v;                /* device */
     int    dtype;            /* PKH_KV_F32 or PKH_KV_F16 */
     int    device;
+    size_t stride_pos;       /* elements between positions p and p+1 of a head */
+    size_t stride_head;      /* elements between KV heads g and g+1 */
 } pkh_kv_t;
 
-/* Replaces pickle_fast_kv_alloc (src/pickle_fast.c:1793-1810): two zeroed
- * device buffers of n_layers * max_seq * n_kv_heads * head_dim elements.
- * PKH_ERR_MEMORY if the device cannot hold them (the struct is zeroed). */
+/* Replaces pickle_fast_kv_alloc (src/pickle_fast.c:1793-1810): one zeroed
+ * device allocation holding K and V, n_layers * max_seq * n_kv_heads *
+ * head_dim elements each, in the head-major layout above.  PKH_ERR_MEMORY
+ * if the device cannot hold it (the struct is zeroed). */
 int  pkh_kv_alloc(int n_layers, int n_kv_heads, int head_dim, int max_seq,
                   int dtype, pkh_kv_t* kv);
 
@@ -91,9 +105,10 @@ int  pkh_kv_alloc(int n_layers, int n_kv_heads, int head_dim, int max_seq,
 void pkh_kv_free(pkh_kv_t* kv);
 
 /* Copy n_pos cache rows of one layer between host and device (dir 0:
- * device -> host, 1: host -> device).  Host rows use the cache's dtype
- * (fp16 as uint16 bit patterns).  For callers that seed or inspect a
- * cache; the reference reads kv->k/v directly (src/pickle_fast.h:153). */
+ * device -> host, 1: host -> device).  Host rows are in the reference's
+ * layout [pos][kv_head][head_dim] and the cache's dtype (fp16 as uint16 bit
+ * patterns), whatever the device strides.  For callers that seed or inspect
+ * a cache; the reference reads kv->k/v directly (src/pickle_fast.h:153). */
 int  pkh_kv_copy_rows(const pkh_kv_t* kv, int which_v, int layer, int pos0,
                       int n_pos, void* host, int dir);
 
@@ -171,9 +186,12 @@ int pkh_attn_prefill_async(const pkh_kv_t* kv, const pkh_rope_t* rope,
 /* ------------------------------------------------------------------ */
 
 /* Several sequences' caches in one allocation: sequence s owns slots
- * [slot0[s], slot0[s] + max_seq[s]) of every layer, each slot one
- * [n_kv_heads][head_dim] row.  No counterpart in the reference, which keeps
- * one sequence per pickle_fast_kv_t (src/pickle_fast.h:140-157). */
+ * [slot0[s], slot0[s] + max_seq[s]) of every layer and KV head, each slot
+ * one head_dim row of K and one of V.  Element (L, s, p, g, d) of K is at
+ *     k + L*layer_stride + g*stride_head + (slot0[s] + p)*stride_pos + d
+ * (V likewise from v).  pkh_kv_batch_alloc uses the head-major layout of
+ * pkh_kv_alloc.  No counterpart in the reference, which keeps one sequence
+ * per pickle_fast_kv_t (src/pickle_fast.h:140-157). */
 typedef struct {
     int      n_layers;
     int      n_kv_heads;
@@ -181,12 +199,14 @@ typedef struct {
     int      n_seqs;
     int      dtype;
     int      device;
-    size_t   layer_stride;   /* elements per layer (all slots) */
+    size_t   layer_stride;   /* elements between layers */
     int64_t* slot0;          /* host [n_seqs + 1], prefix sum of max_seq */
     int*     max_seq;        /* host [n_seqs] */
-    void*    k;              /* device */
+    void*    k;              /* device; the allocation base */
     void*    v;              /* device */
     void*    d_slot0;        /* device copy of slot0 */
+    size_t   stride_pos;
+    size_t   stride_head;
 } pkh_kv_batch_t;
 
 int  pkh_kv_batch_alloc(int n_layers, int n_kv_heads, int head_dim,
@@ -211,7 +231,8 @@ int pkh_attn_decode_batch_async(const pkh_kv_batch_t* kvb,
                                 const float* d_v, float* d_ao, void* stream);
 
 /* Copy n_pos rows of sequence `seq` of one layer between host and device
- * (dir 0: device -> host, 1: host -> device), in the cache's dtype. */
+ * (dir 0: device -> host, 1: host -> device); host rows as for
+ * pkh_kv_copy_rows. */
 int pkh_kv_batch_copy_rows(const pkh_kv_batch_t* kvb, int which_v, int layer,
                            int seq, int pos0, int n_pos, void* host, int dir);
 

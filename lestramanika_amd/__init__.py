@@ -56,6 +56,8 @@ class KV(ctypes.Structure):
         ("v", ctypes.c_void_p),
         ("dtype", ctypes.c_int),
         ("device", ctypes.c_int),
+        ("stride_pos", ctypes.c_size_t),
+        ("stride_head", ctypes.c_size_t),
     ]
 
 
@@ -86,6 +88,8 @@ class KVBatch(ctypes.Structure):
         ("k", ctypes.c_void_p),
         ("v", ctypes.c_void_p),
         ("d_slot0", ctypes.c_void_p),
+        ("stride_pos", ctypes.c_size_t),
+        ("stride_head", ctypes.c_size_t),
     ]
 
 

@@ -64,7 +64,13 @@ int hip_fail(hipError_t e, const char* what) {
 int current_device() { return g_device; }
 
 int scratch_get(size_t bytes, void** out) {
-    return grow(g_scratch[g_device], bytes, out);
+    Buf& b = g_scratch[g_device];
+    const bool fresh = !(bytes <= b.bytes && b.ptr);
+    int rc = grow(b, bytes, out);
+    // A new scratch starts zeroed: the decode kernels keep per-(sequence,
+    // KV head) counters there, which they return to zero themselves.
+    if (rc == PKH_OK && fresh) PKH_HIP(hipMemset(b.ptr, 0, b.bytes));
+    return rc;
 }
 
 int staging_get(int slot, size_t bytes, void** out) {
@@ -100,66 +106,80 @@ extern "C" int pkh_kv_alloc(int n_layers, int n_kv_heads, int head_dim, int max_
     std::memset(kv, 0, sizeof(*kv));
     if (n_layers <= 0 || n_kv_heads <= 0 || head_dim <= 0 || max_seq <= 0) return PKH_ERR_ARG;
     if (dtype != PKH_KV_F32 && dtype != PKH_KV_F16) return PKH_ERR_ARG;
-    size_t stride, total, bytes;
-    if (!mul_ok((size_t)max_seq, (size_t)n_kv_heads * (size_t)head_dim, &stride) ||
-        !mul_ok(stride, (size_t)n_layers, &total) ||
+    // Per layer: [kv_head][pos][K row | V row].
+    size_t head, layer, total, bytes;
+    if (!mul_ok((size_t)max_seq, 2 * (size_t)head_dim, &head) ||
+        !mul_ok(head, (size_t)n_kv_heads, &layer) || !mul_ok(layer, (size_t)n_layers, &total) ||
         !mul_ok(total, elem_size(dtype), &bytes))
         return PKH_ERR_MEMORY;
     PKH_HIP(hipSetDevice(g_device));
-    void* k = nullptr;
-    void* v = nullptr;
-    hipError_t e = hipMalloc(&k, bytes);
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(kv.k)");
-    e = hipMalloc(&v, bytes);
-    if (e != hipSuccess) {
-        (void)hipFree(k);
-        return hip_fail(e, "hipMalloc(kv.v)");
-    }
+    void* base = nullptr;
+    hipError_t e = hipMalloc(&base, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(kv)");
     // The reference's cache is calloc'ed (src/pickle_fast.c:1803-1804).
-    e = hipMemset(k, 0, bytes);
-    if (e == hipSuccess) e = hipMemset(v, 0, bytes);
+    e = hipMemset(base, 0, bytes);
     if (e != hipSuccess) {
-        (void)hipFree(k);
-        (void)hipFree(v);
+        (void)hipFree(base);
         return hip_fail(e, "hipMemset(kv)");
     }
     kv->n_layers = n_layers;
     kv->n_kv_heads = n_kv_heads;
     kv->head_dim = head_dim;
     kv->max_seq = max_seq;
-    kv->k_stride_layer = stride;
-    kv->v_stride_layer = stride;
-    kv->k = k;
-    kv->v = v;
+    kv->k_stride_layer = layer;
+    kv->v_stride_layer = layer;
+    kv->k = base;
+    kv->v = (char*)base + (size_t)head_dim * elem_size(dtype);
     kv->dtype = dtype;
     kv->device = g_device;
+    kv->stride_pos = 2 * (size_t)head_dim;
+    kv->stride_head = head;
     return PKH_OK;
 }
 
 extern "C" void pkh_kv_free(pkh_kv_t* kv) {
     if (!kv) return;
-    if (kv->k || kv->v) {
+    if (kv->k) {
         (void)hipDeviceSynchronize();
-        (void)hipFree(kv->k);
-        (void)hipFree(kv->v);
+        (void)hipFree(kv->k);   // one allocation; v points inside it
     }
     std::memset(kv, 0, sizeof(*kv));
 }
 
+namespace {
+
+// Copy rows [pos0, pos0 + n_pos) of every KV head between a host block in the
+// reference layout [pos][kv_head][head_dim] and a strided device layer.
+int copy_rows_strided(char* dev_layer, size_t stride_pos, size_t stride_head, int n_kv_heads,
+                      int head_dim, size_t es, size_t row0, int n_pos, void* host, int dir) {
+    if (n_pos == 0) return PKH_OK;
+    const size_t width = (size_t)head_dim * es;
+    const size_t hpitch = (size_t)n_kv_heads * head_dim * es;
+    for (int g = 0; g < n_kv_heads; g++) {
+        char* d = dev_layer + ((size_t)g * stride_head + row0 * stride_pos) * es;
+        char* h = (char*)host + (size_t)g * width;
+        if (dir == 0)
+            PKH_HIP(hipMemcpy2D(h, hpitch, d, stride_pos * es, width, (size_t)n_pos,
+                                hipMemcpyDeviceToHost));
+        else
+            PKH_HIP(hipMemcpy2D(d, stride_pos * es, h, hpitch, width, (size_t)n_pos,
+                                hipMemcpyHostToDevice));
+    }
+    return PKH_OK;
+}
+
+}  // namespace
+
 extern "C" int pkh_kv_copy_rows(const pkh_kv_t* kv, int which_v, int layer, int pos0,
                                 int n_pos, void* host, int dir) {
-    if (!kv || !kv->k || !host || n_pos < 0) return PKH_ERR_ARG;
+    if (!kv || !kv->k || !kv->v || !host || n_pos < 0) return PKH_ERR_ARG;
     if (layer < 0 || layer >= kv->n_layers || pos0 < 0 || pos0 + n_pos > kv->max_seq)
         return PKH_ERR_RANGE;
     const size_t es = elem_size(kv->dtype);
-    const size_t row = (size_t)kv->n_kv_heads * kv->head_dim;
     char* base = (char*)(which_v ? kv->v : kv->k) +
-                 ((size_t)layer * kv->k_stride_layer + (size_t)pos0 * row) * es;
-    const size_t bytes = (size_t)n_pos * row * es;
-    if (bytes == 0) return PKH_OK;
-    if (dir == 0) PKH_HIP(hipMemcpy(host, base, bytes, hipMemcpyDeviceToHost));
-    else          PKH_HIP(hipMemcpy(base, host, bytes, hipMemcpyHostToDevice));
-    return PKH_OK;
+                 (size_t)layer * (which_v ? kv->v_stride_layer : kv->k_stride_layer) * es;
+    return copy_rows_strided(base, kv->stride_pos, kv->stride_head, kv->n_kv_heads, kv->head_dim,
+                             es, (size_t)pos0, n_pos, host, dir);
 }
 
 // ---------------------------------------------------------------------------
@@ -236,6 +256,8 @@ int decode_checked(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer, int po
     const size_t es = elem_size(kv->dtype);
     a.k_layer = (const char*)kv->k + (size_t)layer * kv->k_stride_layer * es;
     a.v_layer = (const char*)kv->v + (size_t)layer * kv->v_stride_layer * es;
+    a.stride_pos = (long long)kv->stride_pos;
+    a.stride_head = (long long)kv->stride_head;
     a.dtype = kv->dtype;
     a.head_dim = D;
     a.n_heads = n_heads;
@@ -257,8 +279,14 @@ int decode_checked(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer, int po
     return launch_decode(a, st);
 }
 
+bool strides_ok(size_t stride_pos, size_t stride_head, int head_dim) {
+    return stride_pos >= (size_t)head_dim && stride_head >= (size_t)head_dim &&
+           stride_pos % 8 == 0 && stride_head % 8 == 0;
+}
+
 int decode_validate(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer, int pos, int n_heads) {
     if (!kv || !kv->k || !kv->v) return PKH_ERR_ARG;
+    if (!strides_ok(kv->stride_pos, kv->stride_head, kv->head_dim)) return PKH_ERR_ARG;
     int rc = check_common(kv->head_dim, n_heads, kv->n_kv_heads, rope);
     if (rc != PKH_OK) return rc;
     if (layer < 0 || layer >= kv->n_layers) return PKH_ERR_RANGE;
@@ -310,6 +338,7 @@ namespace {
 int prefill_validate(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer, int pos0,
                      int n_tokens, int n_heads) {
     if (!kv || !kv->k || !kv->v) return PKH_ERR_ARG;
+    if (!strides_ok(kv->stride_pos, kv->stride_head, kv->head_dim)) return PKH_ERR_ARG;
     int rc = check_common(kv->head_dim, n_heads, kv->n_kv_heads, rope);
     if (rc != PKH_OK) return rc;
     if (!prefill_supported(kv->head_dim, n_heads / kv->n_kv_heads, kv->dtype)) return PKH_ERR_ARG;
@@ -327,6 +356,8 @@ int prefill_checked(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer, int p
     const size_t es = elem_size(kv->dtype);
     a.k_layer = (char*)kv->k + (size_t)layer * kv->k_stride_layer * es;
     a.v_layer = (char*)kv->v + (size_t)layer * kv->v_stride_layer * es;
+    a.stride_pos = (long long)kv->stride_pos;
+    a.stride_head = (long long)kv->stride_head;
     a.dtype = kv->dtype;
     a.head_dim = kv->head_dim;
     a.n_heads = n_heads;
@@ -418,25 +449,24 @@ extern "C" int pkh_kv_batch_alloc(int n_layers, int n_kv_heads, int head_dim, in
         ms[s] = max_seq[s];
         slot0[s + 1] = slot0[s] + max_seq[s];
     }
-    size_t row = (size_t)n_kv_heads * head_dim, stride, total, bytes;
-    if (!mul_ok((size_t)slot0[n_seqs], row, &stride) || !mul_ok(stride, (size_t)n_layers, &total) ||
-        !mul_ok(total, elem_size(dtype), &bytes)) {
+    // Per layer: [kv_head][slot][K row | V row].
+    const size_t slots = (size_t)slot0[n_seqs];
+    size_t head, stride, total, bytes;
+    if (!mul_ok(slots, 2 * (size_t)head_dim, &head) || !mul_ok(head, (size_t)n_kv_heads, &stride) ||
+        !mul_ok(stride, (size_t)n_layers, &total) || !mul_ok(total, elem_size(dtype), &bytes)) {
         std::free(slot0);
         std::free(ms);
         return PKH_ERR_MEMORY;
     }
-    void *k = nullptr, *v = nullptr, *ds = nullptr;
+    void *k = nullptr, *ds = nullptr;
     hipError_t e = hipSetDevice(g_device);
     if (e == hipSuccess) e = hipMalloc(&k, bytes);
-    if (e == hipSuccess) e = hipMalloc(&v, bytes);
     if (e == hipSuccess) e = hipMalloc(&ds, ((size_t)n_seqs + 1) * sizeof(int64_t));
     if (e == hipSuccess) e = hipMemset(k, 0, bytes);
-    if (e == hipSuccess) e = hipMemset(v, 0, bytes);
     if (e == hipSuccess)
         e = hipMemcpy(ds, slot0, ((size_t)n_seqs + 1) * sizeof(int64_t), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         (void)hipFree(k);
-        (void)hipFree(v);
         (void)hipFree(ds);
         std::free(slot0);
         std::free(ms);
@@ -452,17 +482,18 @@ extern "C" int pkh_kv_batch_alloc(int n_layers, int n_kv_heads, int head_dim, in
     kvb->slot0 = slot0;
     kvb->max_seq = ms;
     kvb->k = k;
-    kvb->v = v;
+    kvb->v = (char*)k + (size_t)head_dim * elem_size(dtype);
     kvb->d_slot0 = ds;
+    kvb->stride_pos = 2 * (size_t)head_dim;
+    kvb->stride_head = head;
     return PKH_OK;
 }
 
 extern "C" void pkh_kv_batch_free(pkh_kv_batch_t* kvb) {
     if (!kvb) return;
-    if (kvb->k || kvb->v || kvb->d_slot0) {
+    if (kvb->k || kvb->d_slot0) {
         (void)hipDeviceSynchronize();
-        (void)hipFree(kvb->k);
-        (void)hipFree(kvb->v);
+        (void)hipFree(kvb->k);   // one allocation; v points inside it
         (void)hipFree(kvb->d_slot0);
     }
     std::free(kvb->slot0);
@@ -476,14 +507,9 @@ extern "C" int pkh_kv_batch_copy_rows(const pkh_kv_batch_t* kvb, int which_v, in
     if (layer < 0 || layer >= kvb->n_layers || seq < 0 || seq >= kvb->n_seqs) return PKH_ERR_RANGE;
     if (pos0 < 0 || pos0 + n_pos > kvb->max_seq[seq]) return PKH_ERR_RANGE;
     const size_t es = elem_size(kvb->dtype);
-    const size_t row = (size_t)kvb->n_kv_heads * kvb->head_dim;
-    char* base = (char*)(which_v ? kvb->v : kvb->k) +
-                 ((size_t)layer * kvb->layer_stride + ((size_t)kvb->slot0[seq] + pos0) * row) * es;
-    const size_t bytes = (size_t)n_pos * row * es;
-    if (bytes == 0) return PKH_OK;
-    if (dir == 0) PKH_HIP(hipMemcpy(host, base, bytes, hipMemcpyDeviceToHost));
-    else          PKH_HIP(hipMemcpy(base, host, bytes, hipMemcpyHostToDevice));
-    return PKH_OK;
+    char* base = (char*)(which_v ? kvb->v : kvb->k) + (size_t)layer * kvb->layer_stride * es;
+    return copy_rows_strided(base, kvb->stride_pos, kvb->stride_head, kvb->n_kv_heads,
+                             kvb->head_dim, es, (size_t)kvb->slot0[seq] + pos0, n_pos, host, dir);
 }
 
 extern "C" int pkh_plan_create(const pkh_kv_batch_t* kvb, const int* pos, int n_heads,
@@ -556,6 +582,8 @@ extern "C" int pkh_attn_decode_batch_async(const pkh_kv_batch_t* kvb, const pkh_
     const size_t es = elem_size(kvb->dtype);
     a.k_layer = (const char*)kvb->k + (size_t)layer * kvb->layer_stride * es;
     a.v_layer = (const char*)kvb->v + (size_t)layer * kvb->layer_stride * es;
+    a.stride_pos = (long long)kvb->stride_pos;
+    a.stride_head = (long long)kvb->stride_head;
     a.dtype = kvb->dtype;
     a.head_dim = kvb->head_dim;
     a.n_heads = plan->n_heads;

@@ -46,6 +46,7 @@ namespace pkh {
 namespace {
 
 constexpr float kTau = 8.0f;   // lazy-rescale threshold (log2 units)
+constexpr int kCoherent = 16;  // buffer cache policy: sc1, device-coherent access
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
@@ -56,11 +57,17 @@ template <> struct Elt<_Float16> { static constexpr int EPL = 8; };
 template <int D, int G, typename KT>
 struct Shape {
     static constexpr int EPL = Elt<KT>::EPL;       // elements per 16-byte load
-    static constexpr int F   = (G >= 8) ? 8 : 16;  // elements per lane per row
+    static constexpr int F   = D >= 256 ? 16 : 8;  // elements per lane per row
     static constexpr int LPP = D / F;              // lanes per row
     static constexpr int PPW = 64 / LPP;           // rows per wave tile
     static constexpr int NLD = F / EPL;            // loads per lane per row
     static constexpr int S   = EPL * LPP;          // element stride between a lane's loads
+    // Tiles in flight per wave, enough bytes outstanding to cover HBM
+    // latency; MINW is the waves per SIMD the register budget is sized for
+    // (the largest query groups hold 2*G*F accumulator and query registers
+    // and run one wave per SIMD).
+    static constexpr int DEPTH = 4;
+    static constexpr int MINW = (G >= 8 || (G >= 4 && D >= 256)) ? 1 : 2;
     static_assert(D % F == 0 && LPP >= 1 && LPP <= 16, "row split");
     static_assert(F % EPL == 0, "whole loads per lane");
 };
@@ -135,31 +142,37 @@ __device__ __forceinline__ void load_row(uint4 (&r)[NLD], const KT* row, int j) 
         r[i] = *reinterpret_cast<const uint4*>(row + EPL * j + S * i);
 }
 
-// Rotate EPL consecutive elements starting at element b of one head vector x
-// (fp32, global) by table row (sn, cs); half = rotation half-width.  Element
-// i < half becomes fma(c, x[i], -(s*x[i+half])) and element i + half becomes
-// fma(s, x[i], c*x[i+half]): the evaluation of src/pickle_fast.c:1922-1933
-// in the reference's default FMA build, so rotated values match it bit for bit.
+// Rotate the EPL consecutive elements starting at element b of one head
+// vector x (fp32, global) by table row (sn, cs); half = rotation half-width.
+// Element i < half becomes fma(c, x[i], -(s*x[i+half])) and element i + half
+// becomes fma(s, x[i], c*x[i+half]): the evaluation of
+// src/pickle_fast.c:1922-1933 in the reference's default FMA build, so the
+// rotated values match it bit for bit.  A block never straddles `half` (both
+// are multiples of 4), so the branch-free selects below act per block; all
+// loads are 16-byte vectors.
 template <int EPL>
 __device__ __forceinline__ void rope_block(float (&out)[EPL], const float* x, int b, int half,
                                            const float* sn, const float* cs) {
-    if (b < half) {
+    const bool lo = b < half;
+    const bool hi = !lo && b < 2 * half;
+    const int pb = lo ? b + half : b - half;              // partner block
+    const int tb = lo ? b : (hi ? b - half : 0);          // table block
 #pragma unroll
-        for (int c = 0; c < EPL; c++) {
-            const float a = x[b + c], bb = x[b + c + half];
-            const float co = cs[b + c], si = sn[b + c];
-            out[c] = __builtin_fmaf(co, a, -__fmul_rn(si, bb));
+    for (int c4 = 0; c4 < EPL; c4 += 4) {
+        const float4 xv = *reinterpret_cast<const float4*>(x + b + c4);
+        const float4 pv = *reinterpret_cast<const float4*>(x + pb + c4);
+        const float4 sv = *reinterpret_cast<const float4*>(sn + tb + c4);
+        const float4 cv = *reinterpret_cast<const float4*>(cs + tb + c4);
+        const float xa[4] = {xv.x, xv.y, xv.z, xv.w};
+        const float pa[4] = {pv.x, pv.y, pv.z, pv.w};
+        const float sa[4] = {sv.x, sv.y, sv.z, sv.w};
+        const float ca[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float r_lo = __builtin_fmaf(ca[c], xa[c], -__fmul_rn(sa[c], pa[c]));
+            const float r_hi = __builtin_fmaf(sa[c], pa[c], __fmul_rn(ca[c], xa[c]));
+            out[c4 + c] = lo ? r_lo : (hi ? r_hi : xa[c]);
         }
-    } else if (b < 2 * half) {
-#pragma unroll
-        for (int c = 0; c < EPL; c++) {
-            const float a = x[b + c - half], bb = x[b + c];
-            const float co = cs[b + c - half], si = sn[b + c - half];
-            out[c] = __builtin_fmaf(si, a, __fmul_rn(co, bb));
-        }
-    } else {
-#pragma unroll
-        for (int c = 0; c < EPL; c++) out[c] = x[b + c];
     }
 }
 
@@ -177,12 +190,15 @@ struct SplitParams {
     float* out;
     float* part_o;            // [total_chunks][H][D]
     float* part_ml;           // [total_chunks][H][2]
+    int* counters;            // [n_seqs][HK] finished chunks; zero between launches
     const float* rope_sin;
     const float* rope_cos;
     const long long* seq_slot0;
     const int* seq_pos;
     const int* chunk_start;
     long long slot0;
+    long long stride_pos;
+    long long stride_head;
     int pos;
     int n_seqs;
     int H, HK, half, chunk;
@@ -190,18 +206,19 @@ struct SplitParams {
 };
 
 template <int D, int G, typename KT, int WAVES, bool RAGGED>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
-void decode_split(SplitParams P) {
+__global__ __launch_bounds__(64 * WAVES)
+__attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(SplitParams P) {
     using SH = Shape<D, G, KT>;
     constexpr int EPL = SH::EPL, F = SH::F, LPP = SH::LPP, PPW = SH::PPW,
-                  NLD = SH::NLD, S = SH::S;
+                  NLD = SH::NLD, S = SH::S, DEPTH = SH::DEPTH;
 
     __shared__ float red_o[WAVES][G][D];
+    __shared__ __attribute__((aligned(16))) float q_lds[G][D];
     __shared__ float red_m[WAVES][G];
     __shared__ float red_l[WAVES][G];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane % LPP;        // slot of this lane inside its row group
     const int grp = lane / LPP;      // row of the tile handled by this lane
     const int g = blockIdx.y;        // KV head
@@ -236,30 +253,17 @@ void decode_split(SplitParams P) {
 
     // Buffer resources over rows [0, p_end) of this sequence's KV head g:
     // loads past p_end return zeros, so partial tiles need no predicate.
-    const size_t row_elems = (size_t)HK * D;
-    const unsigned row_bytes = (unsigned)(row_elems * sizeof(KT));
-    KT* kbase = const_cast<KT*>(reinterpret_cast<const KT*>(P.k_layer)) + (size_t)slot0 * row_elems + (size_t)g * D;
-    KT* vbase = const_cast<KT*>(reinterpret_cast<const KT*>(P.v_layer)) + (size_t)slot0 * row_elems + (size_t)g * D;
-    const int extent = (int)((unsigned)p_end * row_bytes - (unsigned)(g * D * sizeof(KT)));
+    const unsigned row_bytes = (unsigned)(P.stride_pos * (long long)sizeof(KT));
+    const size_t head_off = (size_t)g * P.stride_head + (size_t)slot0 * P.stride_pos;
+    KT* kbase = const_cast<KT*>(reinterpret_cast<const KT*>(P.k_layer)) + head_off;
+    KT* vbase = const_cast<KT*>(reinterpret_cast<const KT*>(P.v_layer)) + head_off;
+    const int extent = (int)((unsigned)p_end * row_bytes);
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(kbase, (short)0, extent, 0x00020000);
     const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(vbase, (short)0, extent, 0x00020000);
     const float* sn = P.rope_sin + (size_t)pos * half;
     const float* cs = P.rope_cos + (size_t)pos * half;
 
-    // Rotated, pre-scaled queries of the G heads of this KV head.
-    float qr[G][F];
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-        const float* qh = P.q + ((size_t)seq * H + (size_t)g * G + h) * D;
-#pragma unroll
-        for (int i = 0; i < NLD; i++) {
-            float blk[EPL];
-            rope_block<EPL>(blk, qh, EPL * j + S * i, half, sn, cs);
-#pragma unroll
-            for (int e = 0; e < EPL; e++) qr[h][EPL * i + e] = blk[e] * P.qscale;
-        }
-    }
-
+    float qr[G][F];           // rotated, pre-scaled queries (filled below)
     float m[G], l[G], acc[G][F];
 #pragma unroll
     for (int h = 0; h < G; h++) {
@@ -323,18 +327,77 @@ void decode_split(SplitParams P) {
         consume(kf, vf, p < p_end && p != pos);
     };
 
-    // Main loop: this wave's tiles t = wave, wave + WAVES, ...; the next
-    // tile's loads are issued before the current one is consumed.
-    {
-        uint4 ka[NLD], va[NLD], kb[NLD], vb[NLD];  // current tile, next tile
-        int t = wave;
-        if (t < n_tiles) issue(t, ka, va);
-        while (t < n_tiles) {
-            if (t + WAVES < n_tiles) issue(t + WAVES, kb, vb);
-            use(t, ka, va);
-            t += WAVES;
+    // Main loop over this wave's tiles t = wave, wave + WAVES, ...: a ring
+    // of DEPTH tiles is in flight; each consumed slot is refilled with the
+    // tile DEPTH steps ahead.  The first DEPTH tiles are issued before the
+    // queries are loaded, so their latency overlaps the query prologue.
+    // Query prologue.  The workgroup rotates its G query heads once: each
+    // thread loads a few elements with their RoPE partners and table entries
+    // (issued ahead of the KV ring, so waiting for them does not wait for
+    // the ring: loads retire in order), the rotated, pre-scaled rows go to
+    // LDS, and every lane then reads its slice from there.
+    constexpr int QE = (G * D + 64 * WAVES - 1) / (64 * WAVES);   // elements per thread
+    float qx[QE], qp[QE], qs[QE], qc[QE];
 #pragma unroll
-            for (int i = 0; i < NLD; i++) { ka[i] = kb[i]; va[i] = vb[i]; }
+    for (int u = 0; u < QE; u++) {
+        const int idx = min((int)threadIdx.x + u * 64 * WAVES, G * D - 1);
+        const int h = idx / D, d = idx % D;
+        const bool lo = d < half;
+        const bool hi = !lo && d < 2 * half;
+        const float* qh = P.q + ((size_t)seq * H + (size_t)g * G + h) * D;
+        qx[u] = qh[d];
+        qp[u] = qh[lo ? d + half : (hi ? d - half : d)];
+        const int ti = lo ? d : (hi ? d - half : 0);
+        qs[u] = sn[ti];
+        qc[u] = cs[ti];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    uint4 kb[DEPTH][NLD], vb[DEPTH][NLD];
+#pragma unroll
+    for (int i = 0; i < DEPTH; i++) {
+        issue(wave + i * WAVES, kb[i], vb[i]);
+        __builtin_amdgcn_sched_barrier(0);   // keep the slots in issue order
+    }
+
+    // Same arithmetic as rope_block: fma(c, x, -(s*x_partner)) below half,
+    // fma(s, x_partner, c*x) in the upper half, identity past 2*half.
+#pragma unroll
+    for (int u = 0; u < QE; u++) {
+        const int idx = (int)threadIdx.x + u * 64 * WAVES;
+        if (idx < G * D) {
+            const int d = idx % D;
+            const bool lo = d < half;
+            const bool hi = !lo && d < 2 * half;
+            const float r_lo = __builtin_fmaf(qc[u], qx[u], -__fmul_rn(qs[u], qp[u]));
+            const float r_hi = __builtin_fmaf(qs[u], qp[u], __fmul_rn(qc[u], qx[u]));
+            q_lds[idx / D][d] = (lo ? r_lo : (hi ? r_hi : qx[u])) * P.qscale;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < G; h++)
+#pragma unroll
+        for (int i = 0; i < NLD; i++)
+#pragma unroll
+            for (int c4 = 0; c4 < EPL; c4 += 4) {
+                const float4 t4 = *reinterpret_cast<const float4*>(&q_lds[h][EPL * j + S * i + c4]);
+                qr[h][EPL * i + c4 + 0] = t4.x;
+                qr[h][EPL * i + c4 + 1] = t4.y;
+                qr[h][EPL * i + c4 + 2] = t4.z;
+                qr[h][EPL * i + c4 + 3] = t4.w;
+            }
+
+    // Loads are unconditional: tiles past the chunk read rows >= p_end,
+    // which the buffer resource returns as zeros without touching memory,
+    // so the loop has no divergent control flow around its loads and the
+    // waits before each use cover only that slot's loads.
+    for (int base = wave; base < n_tiles; base += DEPTH * WAVES) {
+#pragma unroll
+        for (int i = 0; i < DEPTH; i++) {
+            const int t = base + i * WAVES;
+            use(t, kb[i], vb[i]);   // rows past the chunk are masked
+            issue(t + DEPTH * WAVES, kb[i], vb[i]);
         }
     }
 
@@ -347,8 +410,8 @@ void decode_split(SplitParams P) {
             float kf[F], vf[F];
             const float* kh = P.k_new + ((size_t)seq * HK + g) * D;
             const float* vh = P.v_new + ((size_t)seq * HK + g) * D;
-            KT* kdst = kbase + (size_t)pos * row_elems;
-            KT* vdst = vbase + (size_t)pos * row_elems;
+            KT* kdst = kbase + (size_t)pos * P.stride_pos;
+            KT* vdst = vbase + (size_t)pos * P.stride_pos;
 #pragma unroll
             for (int i = 0; i < NLD; i++) {
                 const int b = EPL * j + S * i;
@@ -387,10 +450,17 @@ void decode_split(SplitParams P) {
         }
         if (lane == 0) { red_m[wave][h] = M; red_l[wave][h] = lh; }
     }
+
     __syncthreads();
 
-    // Merge the waves and write the work item's result.
-    for (int idx = threadIdx.x; idx < G * D; idx += 64 * WAVES) {
+    // Merge the waves.  A sequence that fits one chunk is finished here;
+    // otherwise the work item's (max, sum, o) goes to the partial buffer.
+    const int head0 = g * G;
+    constexpr int OPT = (G * D + 64 * WAVES - 1) / (64 * WAVES);   // outputs per thread
+    float Om[OPT], Ol[OPT], Oo[OPT];
+#pragma unroll
+    for (int u = 0; u < OPT; u++) {
+        const int idx = min((int)threadIdx.x + u * 64 * WAVES, G * D - 1);
         const int h = idx / D, d = idx % D;
         float M = -INFINITY;
 #pragma unroll
@@ -403,52 +473,122 @@ void decode_split(SplitParams P) {
             L = fmaf(red_l[w][h], f, L);
             O = fmaf(red_o[w][h][d], f, O);
         }
-        const int head = g * G + h;
-        if (n_chunks == 1) {
-            P.out[((size_t)seq * H + head) * D + d] = O / L;
-        } else {
-            P.part_o[((size_t)gchunk * H + head) * D + d] = O;
-            if (d == 0) {
-                P.part_ml[((size_t)gchunk * H + head) * 2 + 0] = M;
-                P.part_ml[((size_t)gchunk * H + head) * 2 + 1] = L;
+        Om[u] = M;
+        Ol[u] = L;
+        Oo[u] = O;
+    }
+    if (n_chunks == 1) {
+#pragma unroll
+        for (int u = 0; u < OPT; u++) {
+            const int idx = (int)threadIdx.x + u * 64 * WAVES;
+            if (idx < G * D)
+                P.out[((size_t)seq * H + head0 + idx / D) * D + idx % D] = Oo[u] / Ol[u];
+        }
+        return;
+    }
+    // Partials are written and read with device-scope atomic stores and loads,
+    // which go through the per-XCD L2 to the device-coherent level, so the
+    // last work item reads what the others wrote without a cache writeback
+    // or invalidate (a __threadfence here costs a full L2 writeback per
+    // workgroup).
+#pragma unroll
+    for (int u = 0; u < OPT; u++) {
+        const int idx = (int)threadIdx.x + u * 64 * WAVES;
+        if (idx < G * D) {
+            const size_t base = (size_t)gchunk * H + head0 + idx / D;
+            __hip_atomic_store(P.part_o + base * D + idx % D, Oo[u], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            if (idx % D == 0) {
+                __hip_atomic_store(P.part_ml + base * 2 + 0, Om[u], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(P.part_ml + base * 2 + 1, Ol[u], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             }
         }
     }
-}
 
-// ---- combine kernel -----------------------------------------------------
-
-template <int D>
-__global__ __launch_bounds__(64) void decode_combine(const float* __restrict__ part_o,
-                                                     const float* __restrict__ part_ml,
-                                                     const int* __restrict__ chunk_start,
-                                                     int single_chunks, int H,
-                                                     float* __restrict__ out) {
-    constexpr int PER = (D + 63) / 64;
-    const int head = blockIdx.x, seq = blockIdx.y;
-    const int cb = chunk_start ? chunk_start[seq] : 0;
-    const int ce = chunk_start ? chunk_start[seq + 1] : single_chunks;
-    if (ce - cb <= 1) return;   // single-chunk sequences were finished by the split kernel
-    float M = -INFINITY;
-    for (int c = cb; c < ce; c++) M = fmaxf(M, part_ml[((size_t)c * H + head) * 2]);
-    float L = 0.0f, O[PER];
-#pragma unroll
-    for (int i = 0; i < PER; i++) O[i] = 0.0f;
-    for (int c = cb; c < ce; c++) {
-        const size_t base = (size_t)c * H + head;
-        const float f = __builtin_amdgcn_exp2f(part_ml[base * 2] - M);
-        L = fmaf(part_ml[base * 2 + 1], f, L);
-#pragma unroll
-        for (int i = 0; i < PER; i++) {
-            const int d = threadIdx.x + 64 * i;
-            if (d < D) O[i] = fmaf(part_o[base * D + d], f, O[i]);
-        }
+    // Split-K combine, fused: the last work item of (sequence, KV head) to
+    // finish merges all of its chunks.  Each thread waits for its partial
+    // stores to complete before the workgroup takes a ticket; the last one
+    // resets the count for the next launch.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    __shared__ int last;
+    if (threadIdx.x == 0) {
+        int* cnt = P.counters + seq * HK + g;
+        const int t = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = t == n_chunks - 1;
+        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const float inv = 1.0f / L;
+    __syncthreads();
+    if (!last) return;
+    // Final merge: the G*D outputs as float4 columns, the chunks spread over
+    // CGN thread groups so every partial load is in flight at once; the
+    // groups' online (max, sum, o) are then merged through LDS.
+    constexpr int NV = G * D / 4;                       // float4 columns
+    constexpr int CGN = NV >= 64 * WAVES ? 1 : 64 * WAVES / NV;
+    constexpr int CPT = NV >= 64 * WAVES ? NV / (64 * WAVES) : 1;   // columns per thread
+    static_assert(CPT * 64 * WAVES == NV || CGN * NV == 64 * WAVES, "combine split");
+    __shared__ float4 fo[CGN][NV];
+    __shared__ float fm[CGN][G], fl[CGN][G];
+    const int c0 = RAGGED ? P.chunk_start[seq] : 0;
+    const __amdgpu_buffer_rsrc_t pors =
+        __builtin_amdgcn_make_buffer_rsrc(P.part_o, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t pmrs =
+        __builtin_amdgcn_make_buffer_rsrc(P.part_ml, (short)0, 0x7fffffff, 0x00020000);
+    const int cg = (int)threadIdx.x / (NV / CPT < 64 * WAVES ? NV / CPT : 64 * WAVES);
+    const int col0 = ((int)threadIdx.x % (NV / CPT)) * CPT;
 #pragma unroll
-    for (int i = 0; i < PER; i++) {
-        const int d = threadIdx.x + 64 * i;
-        if (d < D) out[((size_t)seq * H + head) * D + d] = O[i] * inv;
+    for (int u = 0; u < CPT; u++) {
+        const int col = col0 + u;
+        const int h = (4 * col) / D;
+        const int head = head0 + h;
+        float M = -INFINITY, L = 0.0f;
+        float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+        for (int c = cg; c < n_chunks; c += CGN) {
+            const size_t base = (size_t)(c0 + c) * H + head;
+            // 16- and 8-byte loads with the device-coherent (sc1) policy.
+            const float4 oc = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                pors, (unsigned)((base * D + (4 * col) % D) * sizeof(float)), 0, kCoherent));
+            const float2 ml = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                pmrs, (unsigned)(base * 2 * sizeof(float)), 0, kCoherent));
+            const float mn = fmaxf(M, ml.x);
+            const float a = (M == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(M - mn);
+            const float b = __builtin_amdgcn_exp2f(ml.x - mn);
+            L = fmaf(L, a, ml.y * b);
+            O.x = fmaf(O.x, a, oc.x * b);
+            O.y = fmaf(O.y, a, oc.y * b);
+            O.z = fmaf(O.z, a, oc.z * b);
+            O.w = fmaf(O.w, a, oc.w * b);
+            M = mn;
+        }
+        fo[cg][col] = O;
+        if ((4 * col) % D == 0) { fm[cg][h] = M; fl[cg][h] = L; }
+    }
+    __syncthreads();
+    for (int col = threadIdx.x; col < NV; col += 64 * WAVES) {
+        const int h = (4 * col) / D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < CGN; i++) M = fmaxf(M, fm[i][h]);
+        float L = 0.0f;
+        float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int i = 0; i < CGN; i++) {
+            const float f = (fm[i][h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(fm[i][h] - M);
+            L = fmaf(fl[i][h], f, L);
+            const float4 oi = fo[i][col];
+            O.x = fmaf(oi.x, f, O.x);
+            O.y = fmaf(oi.y, f, O.y);
+            O.z = fmaf(oi.z, f, O.z);
+            O.w = fmaf(oi.w, f, O.w);
+        }
+        const float inv = 1.0f / L;
+        *reinterpret_cast<float4*>(P.out + ((size_t)seq * H + head0 + h) * D + (4 * col) % D) =
+            make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
     }
 }
 
@@ -465,12 +605,6 @@ int launch_typed(const DecodeArgs& a, const SplitParams& P, int total_chunks, hi
     else
         hipLaunchKernelGGL((decode_split<D, G, KT, kWaves, false>), grid, block, 0, st, P);
     PKH_HIP(hipGetLastError());
-    if (a.max_chunks > 1) {
-        dim3 cgrid(a.n_heads, a.n_seqs);
-        hipLaunchKernelGGL((decode_combine<D>), cgrid, dim3(64), 0, st, P.part_o, P.part_ml,
-                           a.d_chunk_start, total_chunks, a.n_heads, a.out);
-        PKH_HIP(hipGetLastError());
-    }
     return PKH_OK;
 }
 
@@ -500,8 +634,9 @@ bool shape_supported(int head_dim, int group) {
 }
 
 int decode_tile_positions(int head_dim, int group, int dtype) {
+    (void)group;
     (void)dtype;
-    const int F = group >= 8 ? 8 : 16;
+    const int F = head_dim >= 256 ? 16 : 8;
     const int lpp = head_dim / F;
     return (64 / lpp) * kWaves;
 }
@@ -515,11 +650,13 @@ int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
     if (g_chunk_override > 0) {
         chunk = g_chunk_override;
     } else {
-        // Aim for about 2048 resident waves (8 per CU on 256 CUs) with at
-        // least four tiles per wave, so per-item setup stays small.
-        const long long target_items = 2048 / kWaves;
+        // About 160 work items: enough resident waves to keep HBM busy (each
+        // wave keeps DEPTH tiles in flight) while each (sequence, KV head)
+        // has few chunks for the split-K merge at the end.  Measured on the
+        // Llama-3-8B decode shape at 8K context against 64..1024 rows.
+        const long long target_items = 160;
         chunk = (total_rows * n_kv_heads + target_items - 1) / target_items;
-        if (chunk < 4LL * tile) chunk = 4LL * tile;
+        if (chunk < 2LL * tile) chunk = 2LL * tile;
     }
     chunk = (chunk + tile - 1) / tile * tile;
     if (chunk > (long long)max_attend) chunk = ((long long)max_attend + tile - 1) / tile * tile;
@@ -542,6 +679,8 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
     P.seq_pos = a.d_seq_pos;
     P.chunk_start = a.d_chunk_start;
     P.slot0 = a.slot0;
+    P.stride_pos = a.stride_pos;
+    P.stride_head = a.stride_head;
     P.pos = a.pos;
     P.n_seqs = a.n_seqs;
     P.H = H;
@@ -556,16 +695,20 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
     const long long max_rows = a.n_seqs == 1 && !a.d_chunk_start
                                    ? (long long)a.pos + 1
                                    : (long long)a.max_chunks * a.chunk;
-    if (max_rows * a.n_kv_heads * D * elem >= (1LL << 31)) return PKH_ERR_ARG;
+    if ((max_rows + 1) * a.stride_pos * elem >= (1LL << 31)) return PKH_ERR_ARG;
 
     const int total_chunks = a.total_chunks;
     if (a.max_chunks > 1) {
+        // Scratch: [counters, 256 B aligned][part_o][part_ml].  The counters
+        // are zeroed when the scratch is allocated and reset by the kernel.
+        const size_t n_cnt = ((size_t)a.n_seqs * a.n_kv_heads + 63) / 64 * 64;
         const size_t n_o = (size_t)total_chunks * H * D;
         const size_t n_ml = (size_t)total_chunks * H * 2;
         void* ws = nullptr;
-        int rc = scratch_get((n_o + n_ml) * sizeof(float), &ws);
+        int rc = scratch_get(n_cnt * sizeof(int) + (n_o + n_ml) * sizeof(float), &ws);
         if (rc != PKH_OK) return rc;
-        P.part_o = reinterpret_cast<float*>(ws);
+        P.counters = reinterpret_cast<int*>(ws);
+        P.part_o = reinterpret_cast<float*>(P.counters + n_cnt);
         P.part_ml = P.part_o + n_o;
     }
     if (a.dtype == PKH_KV_F32) return launch_kt<float>(a, P, total_chunks, st);

@@ -38,6 +38,8 @@ bool shape_supported(int head_dim, int group);
 struct DecodeArgs {
     const void* k_layer;      // layer base, element type per dtype
     const void* v_layer;
+    long long stride_pos;     // elements between positions of one head
+    long long stride_head;    // elements between heads
     int dtype;                // PKH_KV_F32 / PKH_KV_F16
     int head_dim, n_heads, n_kv_heads;
     int n_seqs;
@@ -72,6 +74,8 @@ int launch_decode(const DecodeArgs& a, hipStream_t stream);
 struct PrefillArgs {
     void* k_layer;            // fp32 or fp16 cache, layer base
     void* v_layer;
+    long long stride_pos;
+    long long stride_head;
     int dtype;
     int head_dim, n_heads, n_kv_heads;
     int pos0, n_tokens;

@@ -68,6 +68,7 @@ def _fake_kv(n_layers=2, HK=2, D=64, max_seq=16, dtype=pk.PKH_KV_F32):
     kv.k_stride_layer = kv.v_stride_layer = max_seq * HK * D
     kv.k = kv.v = 0x1000      # never dereferenced: every call below fails its checks first
     kv.dtype = dtype
+    kv.stride_pos, kv.stride_head = HK * D, D
     return kv
 
 
@@ -97,6 +98,9 @@ def test_argument_checks_return_before_device_work():
     assert dec(kv, rope, 0, 0, 32) == pk.PKH_ERR_ARG         # group 16 unsupported
     assert dec(kv, _fake_rope(half=16), 0, 0, 4) == pk.PKH_ERR_ARG      # table of another D
     assert dec(_fake_kv(D=24), _fake_rope(half=12), 0, 0, 4) == pk.PKH_ERR_ARG
+    bad = _fake_kv()
+    bad.stride_pos = 3                                        # strides that cannot hold a row
+    assert dec(bad, rope, 0, 0, 4) == pk.PKH_ERR_ARG
     assert lib.pkh_attn_decode_async(ctypes.byref(kv), ctypes.byref(rope), 0, 0, 4,
                                      None, dummy, dummy, dummy, None) == pk.PKH_ERR_ARG
     pf = lambda pos0, n: lib.pkh_attn_prefill(ctypes.byref(kv), ctypes.byref(rope), 0, pos0, n,

@@ -205,3 +205,36 @@ def test_decode_async_on_torch_stream_matches_host_entry():
     finally:
         kv.free()
         rope.free()
+
+
+def test_decode_split_combine_alternating_inputs():
+    """Back-to-back decodes of one layer with alternating inputs and several
+    chunk sizes: every result must match the oracle, so a stale split-K
+    partial or a missed last-work-item hand-off would show."""
+    lib = pk.load()
+    H, HK, D, pos = 32, 8, 128, 6000
+    kv = DeviceKV(1, HK, D, pos + 1)
+    rope = DeviceRope(D, 5e5, pos + 1)
+    try:
+        kc = normal(41, (pos + 1, HK, D))
+        vc = normal(42, (pos + 1, HK, D))
+        kv.write(0, 0, 0, kc[:pos])
+        kv.write(1, 0, 0, vc[:pos])
+        sets = [(normal(43 + 3 * i, (H, D)), normal(44 + 3 * i, (HK, D)),
+                 normal(45 + 3 * i, (HK, D))) for i in range(2)]
+        refs = []
+        for q, k, v in sets:
+            kr, vr = kc[:pos + 1].copy(), vc[:pos + 1].copy()
+            refs.append(po.decode_step(kr, vr, pos, q, k, v, rope.sin, rope.cos, 16)[0])
+        for chunk in (0, 64, 256, 1024):
+            lib.pkh_tune_decode_chunk(chunk)
+            for it in range(6):
+                q, k, v = sets[it % 2]
+                ao = decode_host(kv, rope, 0, pos, q, k, v)
+                err = maxerr(ao, refs[it % 2])
+                assert err <= TOL_F32, (chunk, it, err)
+            log(f"chunk {chunk}: 6 alternating calls within tolerance")
+    finally:
+        lib.pkh_tune_decode_chunk(0)
+        kv.free()
+        rope.free()
