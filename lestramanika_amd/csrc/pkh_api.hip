@@ -22,6 +22,7 @@ struct Buf {
 int g_device = 0;
 Buf g_scratch[kMaxDevices];
 Buf g_staging[kMaxDevices][4];
+Buf g_tiles[kMaxDevices];
 
 int grow(Buf& b, size_t bytes, void** out) {
     if (bytes <= b.bytes && b.ptr) {
@@ -76,6 +77,8 @@ int scratch_get(size_t bytes, void** out) {
 int staging_get(int slot, size_t bytes, void** out) {
     return grow(g_staging[g_device][slot], bytes, out);
 }
+
+int tiles_get(size_t bytes, void** out) { return grow(g_tiles[g_device], bytes, out); }
 
 }  // namespace pkh
 

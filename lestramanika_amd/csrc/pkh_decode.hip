@@ -176,8 +176,14 @@ __device__ __forceinline__ void rope_block(float (&out)[EPL], const float* x, in
     }
 }
 
+// Round the fp32 result into the cache type.  For fp16 the empty asm keeps
+// the conversion from being folded into the fused multiply-add that made x
+// (a single rounding straight to fp16); the reference rounds to fp32 first.
 template <typename KT>
-__device__ __forceinline__ KT to_kt(float x) { return (KT)x; }
+__device__ __forceinline__ KT to_kt(float x) {
+    if constexpr (sizeof(KT) == 2) __asm__ volatile("" : "+v"(x));
+    return (KT)x;
+}
 
 // ---- split kernel -------------------------------------------------------
 

@@ -25,6 +25,9 @@ int scratch_get(size_t bytes, void** out);
 // Per-device grow-only staging buffers for the host-pointer entry points.
 int staging_get(int slot, size_t bytes, void** out);
 
+// Per-device grow-only buffer for the fp16 K/V tiles staged by prefill.
+int tiles_get(size_t bytes, void** out);
+
 // Current device of the library.
 int current_device();
 

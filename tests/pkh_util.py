@@ -83,3 +83,14 @@ def decode_host(kv: DeviceKV, rope: DeviceRope, layer, pos, q, k, v) -> np.ndarr
 
 def maxerr(a, b) -> float:
     return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+def prefill_host(kv: DeviceKV, rope: DeviceRope, layer, pos0, q, k, v) -> np.ndarray:
+    lib = pk.load()
+    n, H = q.shape[0], q.shape[1]
+    ao = np.zeros_like(q, dtype=np.float32)
+    q, k, v = (np.ascontiguousarray(a, np.float32) for a in (q, k, v))
+    pk.check(lib.pkh_attn_prefill(kv.ref, rope.ref, layer, pos0, n, H, q.ctypes.data,
+                                  k.ctypes.data, v.ctypes.data, ao.ctypes.data),
+             "pkh_attn_prefill")
+    return ao

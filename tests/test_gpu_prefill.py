@@ -1,0 +1,225 @@
+"""GPU parity of causal prefill (pkh_attn_prefill*) against the oracle's token
+loop, through the C ABI.
+
+Prefill multiplies on fp16 MFMA operands (q, k, v and the softmax weights are
+rounded to fp16; accumulation, the softmax and the output stay fp32), so its
+outputs are held to max-abs 2e-3.  The rows it appends to the cache do not go
+through fp16 for an fp32 cache and are compared bit for bit: k rotated with
+the reference's contraction and v copied, or their fp16 roundings for an fp16
+cache.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import lestramanika_amd as pk
+from oracle import pyoracle as po
+from pkh_util import DeviceKV, DeviceRope, decode_host, log, maxerr, normal, prefill_host
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3          # fp16 operands, fp32 accumulation
+TOL_DECODE = 1e-4   # fp32 decode after a prefill
+
+
+def _inputs(H, HK, D, pos0, n, seed):
+    return (normal(seed, (pos0, HK, D)), normal(seed + 1, (pos0, HK, D)),
+            normal(seed + 2, (n, H, D)), normal(seed + 3, (n, HK, D)),
+            normal(seed + 4, (n, HK, D)))
+
+
+def _oracle_f32(ctx_k, ctx_v, pos0, q, k, v, rope, threads=16):
+    n, HK, D = k.shape
+    kc = np.zeros((pos0 + n, HK, D), np.float32)
+    vc = np.zeros_like(kc)
+    kc[:pos0], vc[:pos0] = ctx_k, ctx_v
+    ao = po.prefill(kc, vc, pos0, q, k, v, rope.sin, rope.cos, threads)
+    return ao, kc, vc
+
+
+def _oracle_f16(ctx_k16, ctx_v16, pos0, q, k, v, rope, threads=16):
+    n, HK, D = k.shape
+    kc = np.zeros((pos0 + n, HK, D), np.uint16)
+    vc = np.zeros_like(kc)
+    kc[:pos0], vc[:pos0] = ctx_k16, ctx_v16
+    ao = np.stack([po.decode_step_f16(kc, vc, pos0 + t, q[t], k[t], v[t], rope.sin, rope.cos,
+                                      threads) for t in range(n)])
+    return ao, kc, vc
+
+
+def _check(H, HK, D, pos0, n, theta, seed, dtype=pk.PKH_KV_F32, layer=0, n_layers=1,
+           max_seq=None):
+    log(f"prefill H{H} HK{HK} D{D} pos0 {pos0} n {n} theta {theta:g} dtype {dtype} "
+        f"seed {seed} layer {layer}/{n_layers}")
+    max_seq = max_seq or pos0 + n
+    ctx_k, ctx_v, q, k, v = _inputs(H, HK, D, pos0, n, seed)
+    kv = DeviceKV(n_layers, HK, D, max_seq, dtype)
+    rope = DeviceRope(D, theta, pos0 + n, max_seq=max_seq)
+    try:
+        if dtype == pk.PKH_KV_F16:
+            ck, cv = po.f32_to_f16_bits(ctx_k), po.f32_to_f16_bits(ctx_v)
+            if pos0:
+                kv.write(0, layer, 0, ck)
+                kv.write(1, layer, 0, cv)
+            ao = prefill_host(kv, rope, layer, pos0, q, k, v)
+            ref, kc, vc = _oracle_f16(ck, cv, pos0, q, k, v, rope)
+        else:
+            if pos0:
+                kv.write(0, layer, 0, ctx_k)
+                kv.write(1, layer, 0, ctx_v)
+            ao = prefill_host(kv, rope, layer, pos0, q, k, v)
+            ref, kc, vc = _oracle_f32(ctx_k, ctx_v, pos0, q, k, v, rope)
+        assert np.array_equal(kv.read(0, layer, 0, pos0 + n), kc), "cache k rows differ"
+        assert np.array_equal(kv.read(1, layer, 0, pos0 + n), vc), "cache v rows differ"
+        err = maxerr(ao, ref)
+        log(f"  max-abs err {err:.3e}")
+        assert err <= TOL
+        return ao, ref, kv, rope
+    except BaseException:
+        kv.free()
+        rope.free()
+        raise
+
+
+def _check_free(*a, **kw):
+    ao, ref, kv, rope = _check(*a, **kw)
+    kv.free()
+    rope.free()
+    return ao, ref
+
+
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_prefill_shape_sweep(D, G):
+    if D == 256 and G == 8:
+        pytest.skip("head_dim 256 supports groups up to 4")
+    HK = 2
+    for pos0, n in ((0, 1), (0, 37), (0, 200), (70, 129), (1000, 65)):
+        _check_free(G * HK, HK, D, pos0, n, 1e4, 300 + D + G + pos0 + n)
+
+
+def test_prefill_llama3_8b_2048():
+    """Llama-3-8B attention shape, 2048-token prompt from position 0, theta 5e5,
+    seed 4: H32 HK8 D128."""
+    _check_free(32, 8, 128, 0, 2048, 5e5, 4)
+
+
+def test_prefill_tinyllama_after_context():
+    """TinyLlama shape H32 HK4 D64: 300 new tokens after 1500 cached rows."""
+    _check_free(32, 4, 64, 1500, 300, 1e4, 51)
+
+
+@pytest.mark.parametrize("D,G", [(16, 2), (64, 8), (128, 4), (256, 1)])
+def test_prefill_fp16_kv(D, G):
+    for pos0, n in ((0, 50), (300, 97)):
+        _check_free(G * 2, 2, D, pos0, n, 5e5, 400 + D + pos0, dtype=pk.PKH_KV_F16)
+
+
+def test_prefill_then_decode_continues():
+    """Decode at pos0 + n after a prefill sees exactly the rows the oracle's
+    token loop appended (fp32 path, decode tolerance)."""
+    H, HK, D, pos0, n = 32, 8, 128, 40, 300
+    ao, ref, kv, rope = _check(H, HK, D, pos0, n, 5e5, 61, max_seq=pos0 + n + 1)
+    try:
+        ctx_k, ctx_v, q, k, v = _inputs(H, HK, D, pos0, n, 61)
+        _, kc, vc = _oracle_f32(ctx_k, ctx_v, pos0, q, k, v, rope)
+        rope2 = DeviceRope(D, 5e5, pos0 + n + 1)
+        qd, kd, vd = normal(71, (H, D)), normal(72, (HK, D)), normal(73, (HK, D))
+        aod = decode_host(kv, rope2, 0, pos0 + n, qd, kd, vd)
+        kc2 = np.concatenate([kc, np.zeros((1, HK, D), np.float32)])
+        vc2 = np.concatenate([vc, np.zeros((1, HK, D), np.float32)])
+        refd, _, _ = po.decode_step(kc2, vc2, pos0 + n, qd, kd, vd, rope2.sin, rope2.cos, 16)
+        rope2.free()
+        err = maxerr(aod, refd)
+        log(f"decode after prefill: max-abs err {err:.3e}")
+        assert err <= TOL_DECODE
+    finally:
+        kv.free()
+        rope.free()
+
+
+def test_prefill_in_two_calls_matches_one():
+    """A prompt prefilled as 130 + 190 tokens leaves the same cache bits as one
+    320-token call, and both outputs are within tolerance of each other."""
+    H, HK, D = 16, 4, 128
+    ctx_k, ctx_v, q, k, v = _inputs(H, HK, D, 0, 320, 81)
+    a = DeviceKV(1, HK, D, 320)
+    b = DeviceKV(1, HK, D, 320)
+    rope = DeviceRope(D, 5e5, 320)
+    try:
+        one = prefill_host(a, rope, 0, 0, q, k, v)
+        two = np.concatenate([prefill_host(b, rope, 0, 0, q[:130], k[:130], v[:130]),
+                              prefill_host(b, rope, 0, 130, q[130:], k[130:], v[130:])])
+        assert np.array_equal(a.read(0, 0, 0, 320), b.read(0, 0, 0, 320))
+        assert np.array_equal(a.read(1, 0, 0, 320), b.read(1, 0, 0, 320))
+        err = maxerr(one, two)
+        log(f"one call vs two calls: max-abs diff {err:.3e}")
+        assert err <= TOL
+    finally:
+        a.free()
+        b.free()
+        rope.free()
+
+
+def test_prefill_other_layers_and_rows_untouched():
+    H, HK, D, pos0, n = 8, 2, 64, 20, 50
+    ao, ref, kv, rope = _check(H, HK, D, pos0, n, 1e4, 91, layer=1, n_layers=3, max_seq=128)
+    try:
+        for L in (0, 2):
+            assert not kv.read(0, L, 0, 128).any() and not kv.read(1, L, 0, 128).any()
+        assert not kv.read(0, 1, pos0 + n, 128 - pos0 - n).any()
+        assert not kv.read(1, 1, pos0 + n, 128 - pos0 - n).any()
+    finally:
+        kv.free()
+        rope.free()
+
+
+def test_prefill_async_on_torch_stream_is_deterministic():
+    """The device-pointer entry on a torch stream gives the host entry's bits,
+    and repeated calls are bit-identical."""
+    import torch
+    lib = pk.load()
+    H, HK, D, n = 32, 8, 128, 700
+    _, _, q, k, v = _inputs(H, HK, D, 0, n, 101)
+    kv = DeviceKV(1, HK, D, n)
+    rope = DeviceRope(D, 5e5, n)
+    try:
+        host = prefill_host(kv, rope, 0, 0, q, k, v)
+        dev = torch.device("cuda")
+        tq, tk, tv = (torch.from_numpy(x).to(dev) for x in (q, k, v))
+        outs = []
+        for _ in range(3):
+            out = torch.empty((n, H, D), dtype=torch.float32, device=dev)
+            s = torch.cuda.current_stream()
+            rc = lib.pkh_attn_prefill_async(kv.ref, rope.ref, 0, 0, n, H, tq.data_ptr(),
+                                            tk.data_ptr(), tv.data_ptr(), out.data_ptr(),
+                                            ctypes.c_void_p(s.cuda_stream))
+            assert rc == 0
+            torch.cuda.synchronize()
+            outs.append(out.cpu().numpy())
+        for o in outs:
+            assert np.array_equal(o, host)
+    finally:
+        kv.free()
+        rope.free()
+
+
+def test_prefill_rejects_bad_ranges():
+    lib = pk.load()
+    kv = DeviceKV(1, 2, 64, 32)
+    rope = DeviceRope(64, 1e4, 32)
+    try:
+        q = np.zeros((8, 4, 64), np.float32)
+        k = np.zeros((8, 2, 64), np.float32)
+        ao = np.zeros_like(q)
+        call = lambda pos0, n: lib.pkh_attn_prefill(kv.ref, rope.ref, 0, pos0, n, 4,
+                                                    q.ctypes.data, k.ctypes.data,
+                                                    k.ctypes.data, ao.ctypes.data)
+        assert call(25, 8) == pk.PKH_ERR_RANGE      # last position 32 >= max_seq
+        assert call(0, 0) == pk.PKH_ERR_ARG
+        assert call(-1, 4) == pk.PKH_ERR_RANGE
+        assert call(24, 8) == pk.PKH_OK
+    finally:
+        kv.free()
+        rope.free()
