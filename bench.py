@@ -46,6 +46,16 @@ WORKLOADS = {
                                                 layers=64, kv="f32", seed=2),
 }
 
+# Causal prefill of a 2048-token prompt from position 0 through the 32
+# attention layers of the Llama-3-8B shape (fp32 cache, fp16 MFMA operands).
+PREFILL_WORKLOADS = {
+    "llama3-8b-prefill-2048": dict(H=32, HK=8, D=128, S=2048, pos0=0, theta=5e5, layers=32,
+                                   kv="f32", seed=4),
+}
+PREFILL_METRIC = "prefill-attn TFLOP/s (causal, useful FLOPs), Llama-3-8B shape, 2048 tokens"
+MFMA_F16_PEAK_TFLOPS = 2500.0
+PREFILL_TOL = 2e-3
+
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
@@ -241,6 +251,150 @@ def run_decode(args, cfg):
     return result
 
 
+def prefill_flops(H: int, D: int, S: int, pos0: int = 0) -> int:
+    """Useful causal FLOPs: QK^T and PV over the n*(n+1)/2 (plus context)
+    query-key pairs, 2 FLOPs per multiply-add, exp not counted."""
+    pairs = S * pos0 + S * (S + 1) // 2
+    return 4 * D * H * pairs
+
+
+def cpu_baseline_prefill(q, k, v, cfg, threads):
+    """The oracle's token loop (the reference's prefill: one decode step per
+    prompt token) on one layer of the workload."""
+    from oracle import pyoracle as po
+    H, HK, D, S = cfg["H"], cfg["HK"], cfg["D"], cfg["S"]
+    _, sin, cos = po.rope_tables(D, cfg["theta"], S)
+    qq, kk, vv = q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()
+    kc = np.zeros((S, HK, D), np.float32)
+    vc = np.zeros_like(kc)
+    t0 = time.perf_counter()
+    ao = po.prefill(kc, vc, 0, qq, kk, vv, sin, cos, threads)
+    return time.perf_counter() - t0, ao
+
+
+def run_prefill(args, cfg, name):
+    import torch
+    import lestramanika_amd as pk
+    from oracle import pyoracle as po
+
+    torch.cuda.set_device(0)
+    lib = pk.load()
+    pk.check(lib.pkh_init(0), "pkh_init")
+    H, HK, D, S, L = cfg["H"], cfg["HK"], cfg["D"], cfg["S"], cfg["layers"]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(cfg["seed"])
+    log(f"bench: prefill {name}: {L} layers, {S} tokens, H{H} HK{HK} D{D}")
+    KV = torch.zeros((L, HK, S, 2, D), dtype=torch.float32, device=dev)
+    q = torch.randn((L, S, H, D), generator=gen, device=dev)
+    k = torch.randn((L, S, HK, D), generator=gen, device=dev)
+    v = torch.randn((L, S, HK, D), generator=gen, device=dev)
+    ao = torch.zeros((L, S, H, D), device=dev)
+
+    kv = pk.KV()
+    kv.n_layers, kv.n_kv_heads, kv.head_dim, kv.max_seq = L, HK, D, S
+    kv.k_stride_layer = kv.v_stride_layer = HK * S * 2 * D
+    kv.k, kv.v = KV.data_ptr(), KV.data_ptr() + D * 4
+    kv.dtype, kv.device = pk.PKH_KV_F32, 0
+    kv.stride_pos, kv.stride_head = 2 * D, S * 2 * D
+    half = min(D // 2, 64)
+    sin = np.zeros((S, half), np.float32)
+    cos = np.zeros((S, half), np.float32)
+    lib.pkh_rope_host_tables(D, cfg["theta"], 0, S - 1, None, sin.ctypes.data, cos.ctypes.data)
+    rope = pk.Rope()
+    pk.check(lib.pkh_rope_alloc(S, half, ctypes.byref(rope)), "pkh_rope_alloc")
+    pk.check(lib.pkh_rope_upload(ctypes.byref(rope), sin.ctypes.data, cos.ctypes.data, S),
+             "pkh_rope_upload")
+    kvp, rp = ctypes.byref(kv), ctypes.byref(rope)
+    call = lib.pkh_attn_prefill_async
+
+    def step(stream):
+        sp = ctypes.c_void_p(stream.cuda_stream)
+        for layer in range(L):
+            rc = call(kvp, rp, layer, cfg["pos0"], S, H, q[layer].data_ptr(),
+                      k[layer].data_ptr(), v[layer].data_ptr(), ao[layer].data_ptr(), sp)
+            if rc != 0:
+                raise pk.PkhError(rc, "pkh_attn_prefill_async")
+
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        step(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(torch.cuda.current_stream())
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps // 4)
+    log(f"bench: timing {steps} graph replays x {L} layer prefills")
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1 in evs:
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    durs = np.array([e0.elapsed_time(e1) for e0, e1 in evs]) * 1e-3 / L
+    fl = prefill_flops(H, D, S, cfg["pos0"])
+    value = fl * steps * L / wall / 1e12
+    avg_launch = float(durs.mean())
+    achieved = fl / avg_launch / 1e12
+
+    cpu = None
+    errs = []
+    threads = min(16, os.cpu_count() or 1)
+    if not args.no_cpu_baseline:
+        log(f"bench: CPU baseline (oracle token loop, {threads} threads, 1 layer)")
+        t_cpu, ref0 = cpu_baseline_prefill(q[0], k[0], v[0], cfg, threads)
+        errs.append(float(np.max(np.abs(ao[0].cpu().numpy() - ref0))))
+        cpu = {"value": round(fl / t_cpu / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+               "kind": "port",
+               "sample": (f"one layer's {S}-token causal prefill of the same workload with the "
+                          f"oracle's token loop (one restated reference decode step per "
+                          f"token, oracle/pk_oracle.c)"),
+               "us_per_layer": round(t_cpu * 1e6, 1)}
+    for layer in sorted({L - 1} | (set() if errs else {0})):
+        _, osin, ocos = po.rope_tables(D, cfg["theta"], S)
+        kc = np.zeros((S, HK, D), np.float32)
+        vc = np.zeros_like(kc)
+        ref = po.prefill(kc, vc, 0, q[layer].cpu().numpy(), k[layer].cpu().numpy(),
+                         v[layer].cpu().numpy(), osin, ocos, threads)
+        errs.append(float(np.max(np.abs(ao[layer].cpu().numpy() - ref))))
+    log(f"bench: prefill max-abs err vs oracle: {max(errs):.3e} (tolerance {PREFILL_TOL})")
+    lib.pkh_rope_free(rp)
+    return {
+        "metric": PREFILL_METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 MFMA operands, f32 accumulate/softmax/cache",
+        "data": "synthetic: N(0,1) from torch's CUDA generator, seeded per workload",
+        "config": {"workload": name, "n_heads": H, "n_kv_heads": HK, "head_dim": D,
+                   "tokens": S, "pos0": cfg["pos0"], "layers": L, "kv_dtype": cfg["kv"],
+                   "rope_theta": cfg["theta"]},
+        "us_per_layer": round(wall / (steps * L) * 1e6, 3),
+        "flops_per_layer": fl,
+        "pct_mfma_peak": round(100.0 * value / MFMA_F16_PEAK_TFLOPS, 2),
+        "max_abs_err_vs_oracle": max(errs),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
+                     "traffic": traffic_from_profiles(name),
+                     "us_per_launch": round(avg_launch * 1e6, 3)},
+        "cpu_baseline": cpu,
+    }
+
+
 def run_copy_calibration(args):
     """A plain device copy of known size, for scaling the PMC byte counters."""
     import torch
@@ -260,7 +414,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="llama3-8b-decode-ctx8192",
-                    choices=sorted(WORKLOADS) + ["copy-calibration"])
+                    choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS) + ["copy-calibration"])
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the prefill measurement appended to the decode line")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=32,
                     help="layers in the CPU-baseline sample")
@@ -272,7 +428,16 @@ def main():
     if args.workload == "copy-calibration":
         run_copy_calibration(args)
         return
-    res = run_decode(args, WORKLOADS[args.workload])
+    if args.workload in PREFILL_WORKLOADS:
+        res = run_prefill(args, PREFILL_WORKLOADS[args.workload], args.workload)
+    else:
+        res = run_decode(args, WORKLOADS[args.workload])
+        if not args.no_secondary and args.workload == "llama3-8b-decode-ctx8192":
+            name = "llama3-8b-prefill-2048"
+            sec = run_prefill(args, PREFILL_WORKLOADS[name], name)
+            res["secondary"] = {name: {k: sec[k] for k in (
+                "metric", "value", "unit", "us_per_layer", "pct_mfma_peak",
+                "max_abs_err_vs_oracle", "roofline", "cpu_baseline", "config", "dtype")}}
     print(json.dumps(res), flush=True)
 
 
