@@ -94,3 +94,49 @@ def prefill_host(kv: DeviceKV, rope: DeviceRope, layer, pos0, q, k, v) -> np.nda
                                   k.ctypes.data, v.ctypes.data, ao.ctypes.data),
              "pkh_attn_prefill")
     return ao
+
+
+class DeviceKVBatch:
+    """A pkh_kv_batch_t owned by a test: several sequences' caches."""
+
+    def __init__(self, n_layers, n_kv_heads, head_dim, max_seq, dtype=pk.PKH_KV_F32):
+        import ctypes as ct
+        self.lib = pk.load()
+        self.kvb = pk.KVBatch()
+        ms = (ct.c_int * len(max_seq))(*max_seq)
+        pk.check(self.lib.pkh_kv_batch_alloc(n_layers, n_kv_heads, head_dim, len(max_seq), ms,
+                                             dtype, ct.byref(self.kvb)), "pkh_kv_batch_alloc")
+
+    @property
+    def ref(self):
+        return ctypes.byref(self.kvb)
+
+    def write(self, which_v, layer, seq, pos0, rows: np.ndarray):
+        rows = np.ascontiguousarray(rows)
+        pk.check(self.lib.pkh_kv_batch_copy_rows(self.ref, which_v, layer, seq, pos0,
+                                                 rows.shape[0], rows.ctypes.data, 1),
+                 "pkh_kv_batch_copy_rows")
+
+    def read(self, which_v, layer, seq, pos0, n) -> np.ndarray:
+        dt = np.uint16 if self.kvb.dtype == pk.PKH_KV_F16 else np.float32
+        out = np.zeros((n, self.kvb.n_kv_heads, self.kvb.head_dim), dt)
+        pk.check(self.lib.pkh_kv_batch_copy_rows(self.ref, which_v, layer, seq, pos0, n,
+                                                 out.ctypes.data, 0), "pkh_kv_batch_copy_rows")
+        return out
+
+    def free(self):
+        self.lib.pkh_kv_batch_free(self.ref)
+
+
+class Plan:
+    """A pkh_plan_t for one decode step of every sequence."""
+
+    def __init__(self, kvb: DeviceKVBatch, pos, n_heads):
+        self.lib = pk.load()
+        self.ptr = ctypes.c_void_p()
+        arr = (ctypes.c_int * len(pos))(*pos)
+        pk.check(self.lib.pkh_plan_create(kvb.ref, arr, n_heads, ctypes.byref(self.ptr)),
+                 "pkh_plan_create")
+
+    def free(self):
+        self.lib.pkh_plan_free(self.ptr)
