@@ -52,6 +52,14 @@ PREFILL_WORKLOADS = {
     "llama3-8b-prefill-2048": dict(H=32, HK=8, D=128, S=2048, pos0=0, theta=5e5, layers=32,
                                    kv="f32", seed=4),
 }
+# One decode step of 16 sequences with contexts drawn from U[4096, 32768]
+# (numpy default_rng(5)) over the 32 layers of the Llama-3-8B shape, fp16 KV.
+RAGGED_WORKLOADS = {
+    "llama3-8b-ragged16-fp16": dict(H=32, HK=8, D=128, n_seqs=16, ctx_lo=4096, ctx_hi=32768,
+                                    ctx_seed=5, theta=5e5, layers=32, kv="f16", seed=5),
+}
+RAGGED_METRIC = "ragged-decode KV GB/s (% HBM peak), 16 sequences 4K-32K, Llama-3-8B shape, fp16 KV"
+
 PREFILL_METRIC = "prefill-attn TFLOP/s (causal, useful FLOPs), Llama-3-8B shape, 2048 tokens"
 MFMA_F16_PEAK_TFLOPS = 2500.0
 PREFILL_TOL = 2e-3
@@ -395,6 +403,162 @@ def run_prefill(args, cfg, name):
     }
 
 
+def cpu_baseline_ragged(KV, ctx, slot0, q, k, v, cfg, threads):
+    """The oracle's single-sequence fp16 decode step, looped over the
+    sequences (the reference has no batch API), on host copies of layer 0."""
+    from oracle import pyoracle as po
+    H, HK, D = cfg["H"], cfg["HK"], cfg["D"]
+    _, sin, cos = po.rope_tables(D, cfg["theta"], max(ctx) + 1)
+    lay = KV[0].cpu().numpy().view(np.uint16)          # [HK][slots][2][D]
+    host = []
+    for s, c in enumerate(ctx):
+        rows = lay[:, slot0[s]:slot0[s] + c + 1]       # [HK][c+1][2][D]
+        kc = np.ascontiguousarray(rows[:, :, 0].transpose(1, 0, 2))
+        vc = np.ascontiguousarray(rows[:, :, 1].transpose(1, 0, 2))
+        host.append((kc, vc))
+    qq, kk, vv = q[0].cpu().numpy(), k[0].cpu().numpy(), v[0].cpu().numpy()
+    outs = []
+    t0 = time.perf_counter()
+    for s, c in enumerate(ctx):
+        kc, vc = host[s]
+        outs.append(po.decode_step_f16(kc, vc, c, qq[s], kk[s], vv[s], sin, cos, threads))
+    return time.perf_counter() - t0, np.stack(outs)
+
+
+def run_ragged(args, cfg, name):
+    import torch
+    import lestramanika_amd as pk
+
+    torch.cuda.set_device(0)
+    lib = pk.load()
+    pk.check(lib.pkh_init(0), "pkh_init")
+    H, HK, D, L, n = cfg["H"], cfg["HK"], cfg["D"], cfg["layers"], cfg["n_seqs"]
+    ctx = np.random.default_rng(cfg["ctx_seed"]).integers(
+        cfg["ctx_lo"], cfg["ctx_hi"], size=n, endpoint=True).tolist()
+    slot0 = np.zeros(n + 1, np.int64)
+    slot0[1:] = np.cumsum([c + 1 for c in ctx])
+    slots = int(slot0[-1])
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(cfg["seed"])
+    log(f"bench: ragged {name}: {n} sequences, sum(ctx) = {sum(ctx)}, {L} layers, fp16 KV "
+        f"({L * HK * slots * 2 * D * 2 / 1e9:.1f} GB)")
+    # Caller-owned pkh_kv_batch_t over torch's buffer, in the library's
+    # layout: each layer [kv_head][slot][K row | V row].
+    KV = torch.empty((L, HK, slots, 2, D), dtype=torch.float16, device=dev)
+    for layer in range(L):
+        KV[layer].normal_(generator=gen)
+    q = torch.randn((L, n, H, D), generator=gen, device=dev)
+    k = torch.randn((L, n, HK, D), generator=gen, device=dev)
+    v = torch.randn((L, n, HK, D), generator=gen, device=dev)
+    ao = torch.zeros((L, n, H, D), device=dev)
+    d_slot0 = torch.from_numpy(slot0).to(dev)
+    h_slot0 = (ctypes.c_int64 * (n + 1))(*slot0.tolist())
+    h_max = (ctypes.c_int * n)(*[c + 1 for c in ctx])
+    kvb = pk.KVBatch()
+    kvb.n_layers, kvb.n_kv_heads, kvb.head_dim, kvb.n_seqs = L, HK, D, n
+    kvb.dtype, kvb.device = pk.PKH_KV_F16, 0
+    kvb.layer_stride = HK * slots * 2 * D
+    kvb.slot0 = ctypes.cast(h_slot0, ctypes.POINTER(ctypes.c_int64))
+    kvb.max_seq = ctypes.cast(h_max, ctypes.POINTER(ctypes.c_int))
+    kvb.k, kvb.v = KV.data_ptr(), KV.data_ptr() + D * 2
+    kvb.d_slot0 = d_slot0.data_ptr()
+    kvb.stride_pos, kvb.stride_head = 2 * D, slots * 2 * D
+
+    max_seq = max(ctx) + 1
+    half = min(D // 2, 64)
+    sin = np.zeros((max_seq, half), np.float32)
+    cos = np.zeros((max_seq, half), np.float32)
+    lib.pkh_rope_host_tables(D, cfg["theta"], 0, max_seq - 1, None, sin.ctypes.data,
+                             cos.ctypes.data)
+    rope = pk.Rope()
+    pk.check(lib.pkh_rope_alloc(max_seq, half, ctypes.byref(rope)), "pkh_rope_alloc")
+    pk.check(lib.pkh_rope_upload(ctypes.byref(rope), sin.ctypes.data, cos.ctypes.data,
+                                 max_seq), "pkh_rope_upload")
+    plan = ctypes.c_void_p()
+    pk.check(lib.pkh_plan_create(ctypes.byref(kvb), (ctypes.c_int * n)(*ctx), H,
+                                 ctypes.byref(plan)), "pkh_plan_create")
+    kvp, rp = ctypes.byref(kvb), ctypes.byref(rope)
+    call = lib.pkh_attn_decode_batch_async
+
+    def step(stream):
+        sp = ctypes.c_void_p(stream.cuda_stream)
+        for layer in range(L):
+            rc = call(kvp, rp, plan, layer, q[layer].data_ptr(), k[layer].data_ptr(),
+                      v[layer].data_ptr(), ao[layer].data_ptr(), sp)
+            if rc != 0:
+                raise pk.PkhError(rc, "pkh_attn_decode_batch_async")
+
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        step(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(torch.cuda.current_stream())
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps // 2)
+    log(f"bench: timing {steps} graph replays x {L} layers")
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for e0, e1 in evs:
+        e0.record(stream)
+        graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    durs = np.array([e0.elapsed_time(e1) for e0, e1 in evs]) * 1e-3 / L
+    bpl = sum(decode_bytes(c, H, HK, D, 2) for c in ctx)
+    value = bpl * steps * L / wall / 1e9
+    avg_launch = float(durs.mean())
+    achieved = bpl / avg_launch / 1e9
+
+    threads = min(16, os.cpu_count() or 1)
+    log(f"bench: ragged parity + CPU baseline (oracle, {threads} threads, layer 0)")
+    t_cpu, ref = cpu_baseline_ragged(KV, ctx, slot0, q, k, v, cfg, threads)
+    err = float(np.max(np.abs(ao[0].cpu().numpy() - ref)))
+    log(f"bench: ragged max-abs err vs oracle: {err:.3e}")
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = {"value": round(bpl / t_cpu / 1e9, 3), "unit": "GB/s", "cores": threads,
+               "kind": "port",
+               "sample": (f"one layer of the same step: the oracle's fp16-KV decode step "
+                          f"looped over the {n} sequences (oracle/pk_oracle.c)"),
+               "us_per_layer_step": round(t_cpu * 1e6, 1)}
+    lib.pkh_plan_free(plan)
+    lib.pkh_rope_free(rp)
+    return {
+        "metric": RAGGED_METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 KV, f32 arithmetic",
+        "data": "synthetic: N(0,1) from torch's CUDA generator, seeded per workload",
+        "config": {"workload": name, "n_heads": H, "n_kv_heads": HK, "head_dim": D,
+                   "n_seqs": n, "contexts": ctx, "layers": L, "kv_dtype": cfg["kv"],
+                   "rope_theta": cfg["theta"]},
+        "us_per_layer_step": round(wall / (steps * L) * 1e6, 3),
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "bytes_per_layer_step": bpl,
+        "max_abs_err_vs_oracle": err,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles(name),
+                     "us_per_launch": round(avg_launch * 1e6, 3)},
+        "cpu_baseline": cpu,
+    }
+
+
 def run_copy_calibration(args):
     """A plain device copy of known size, for scaling the PMC byte counters."""
     import torch
@@ -414,9 +578,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="llama3-8b-decode-ctx8192",
-                    choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS) + ["copy-calibration"])
+                    choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS) + sorted(RAGGED_WORKLOADS)
+                    + ["copy-calibration"])
     ap.add_argument("--no-secondary", action="store_true",
-                    help="skip the prefill measurement appended to the decode line")
+                    help="skip the prefill and ragged measurements appended to the decode line")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=32,
                     help="layers in the CPU-baseline sample")
@@ -430,14 +595,21 @@ def main():
         return
     if args.workload in PREFILL_WORKLOADS:
         res = run_prefill(args, PREFILL_WORKLOADS[args.workload], args.workload)
+    elif args.workload in RAGGED_WORKLOADS:
+        res = run_ragged(args, RAGGED_WORKLOADS[args.workload], args.workload)
     else:
         res = run_decode(args, WORKLOADS[args.workload])
         if not args.no_secondary and args.workload == "llama3-8b-decode-ctx8192":
-            name = "llama3-8b-prefill-2048"
-            sec = run_prefill(args, PREFILL_WORKLOADS[name], name)
-            res["secondary"] = {name: {k: sec[k] for k in (
-                "metric", "value", "unit", "us_per_layer", "pct_mfma_peak",
-                "max_abs_err_vs_oracle", "roofline", "cpu_baseline", "config", "dtype")}}
+            import torch
+            keep = ("metric", "value", "unit", "pct_mfma_peak", "pct_hbm_peak", "us_per_layer",
+                    "us_per_layer_step", "max_abs_err_vs_oracle", "roofline", "cpu_baseline",
+                    "config", "dtype")
+            res["secondary"] = {}
+            for name, fn, table in (("llama3-8b-prefill-2048", run_prefill, PREFILL_WORKLOADS),
+                                    ("llama3-8b-ragged16-fp16", run_ragged, RAGGED_WORKLOADS)):
+                torch.cuda.empty_cache()
+                sec = fn(args, table[name], name)
+                res["secondary"][name] = {k: sec[k] for k in keep if k in sec}
     print(json.dumps(res), flush=True)
 
 
