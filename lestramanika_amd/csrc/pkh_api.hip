@@ -23,6 +23,7 @@ int g_device = 0;
 Buf g_scratch[kMaxDevices];
 Buf g_staging[kMaxDevices][4];
 Buf g_tiles[kMaxDevices];
+Buf g_counters[kMaxDevices];
 
 int grow(Buf& b, size_t bytes, void** out) {
     if (bytes <= b.bytes && b.ptr) {
@@ -64,14 +65,22 @@ int hip_fail(hipError_t e, const char* what) {
 
 int current_device() { return g_device; }
 
-int scratch_get(size_t bytes, void** out) {
-    Buf& b = g_scratch[g_device];
+int scratch_get(size_t bytes, void** out) { return grow(g_scratch[g_device], bytes, out); }
+
+int counters_get(size_t n, int** out) {
+    Buf& b = g_counters[g_device];
+    const size_t bytes = n * sizeof(int);
     const bool fresh = !(bytes <= b.bytes && b.ptr);
-    int rc = grow(b, bytes, out);
-    // A new scratch starts zeroed: the decode kernels keep per-(sequence,
-    // KV head) counters there, which they return to zero themselves.
-    if (rc == PKH_OK && fresh) PKH_HIP(hipMemset(b.ptr, 0, b.bytes));
-    return rc;
+    void* p = nullptr;
+    int rc = grow(b, bytes, &p);
+    if (rc != PKH_OK) return rc;
+    if (fresh) {
+        // A new counter buffer starts zeroed, before any kernel can use it.
+        PKH_HIP(hipMemset(b.ptr, 0, b.bytes));
+        PKH_HIP(hipDeviceSynchronize());
+    }
+    *out = static_cast<int*>(p);
+    return PKH_OK;
 }
 
 int staging_get(int slot, size_t bytes, void** out) {

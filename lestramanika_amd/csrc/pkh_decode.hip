@@ -705,16 +705,16 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
 
     const int total_chunks = a.total_chunks;
     if (a.max_chunks > 1) {
-        // Scratch: [counters, 256 B aligned][part_o][part_ml].  The counters
-        // are zeroed when the scratch is allocated and reset by the kernel.
-        const size_t n_cnt = ((size_t)a.n_seqs * a.n_kv_heads + 63) / 64 * 64;
+        // Scratch: [part_o][part_ml]; one finished-chunk counter per
+        // (sequence, KV head) in the zero-between-launches counter array.
         const size_t n_o = (size_t)total_chunks * H * D;
         const size_t n_ml = (size_t)total_chunks * H * 2;
         void* ws = nullptr;
-        int rc = scratch_get(n_cnt * sizeof(int) + (n_o + n_ml) * sizeof(float), &ws);
+        int rc = scratch_get((n_o + n_ml) * sizeof(float), &ws);
         if (rc != PKH_OK) return rc;
-        P.counters = reinterpret_cast<int*>(ws);
-        P.part_o = reinterpret_cast<float*>(P.counters + n_cnt);
+        rc = counters_get((size_t)a.n_seqs * a.n_kv_heads, &P.counters);
+        if (rc != PKH_OK) return rc;
+        P.part_o = reinterpret_cast<float*>(ws);
         P.part_ml = P.part_o + n_o;
     }
     if (a.dtype == PKH_KV_F32) return launch_kt<float>(a, P, total_chunks, st);

@@ -22,6 +22,12 @@ int hip_fail(hipError_t e, const char* what);
 // Per-device grow-only scratch owned by the library (split-K partials).
 int scratch_get(size_t bytes, void** out);
 
+// Per-device grow-only array of n ints that is zero between launches: it is
+// zeroed when (re)allocated, and every kernel that counts in it returns the
+// counts it used to zero before it exits.  Kept apart from the scratch so
+// that partials of one launch never land where a later launch counts.
+int counters_get(size_t n, int** out);
+
 // Per-device grow-only staging buffers for the host-pointer entry points.
 int staging_get(int slot, size_t bytes, void** out);
 

@@ -165,3 +165,31 @@ def test_ragged_rejects_bad_plans():
                                           0) == pk.PKH_ERR_RANGE              # no sequence 2
     finally:
         kvb.free()
+
+
+def test_ragged_after_split_decode_with_fewer_counters():
+    """A single-sequence decode split into many chunks (its partials fill the
+    scratch), then a ragged step that needs more (sequence, KV head)
+    counters than that decode did: the ragged step must still match the
+    oracle, i.e. partials of one launch never land where another counts."""
+    from pkh_util import DeviceKV, decode_host, normal
+    lib = pk.load()
+    try:
+        lib.pkh_tune_decode_chunk(64)
+        H, HK, D, pos = 4, 1, 128, 4000
+        kv = DeviceKV(1, HK, D, pos + 1)
+        rope = DeviceRope(D, 5e5, pos + 1)
+        try:
+            kc, vc = normal(61, (pos + 1, HK, D)), normal(62, (pos + 1, HK, D))
+            kv.write(0, 0, 0, kc[:pos])
+            kv.write(1, 0, 0, vc[:pos])
+            q, k, v = normal(63, (H, D)), normal(64, (HK, D)), normal(65, (HK, D))
+            ao = decode_host(kv, rope, 0, pos, q, k, v)
+            ref, _, _ = po.decode_step(kc, vc, pos, q, k, v, rope.sin, rope.cos, 16)
+            assert maxerr(ao, ref) <= TOL_F32
+        finally:
+            kv.free()
+            rope.free()
+        _check(32, 8, 128, [900, 3000, 1500, 64, 2200, 700, 4000, 10] * 2, 5e5, 66)
+    finally:
+        lib.pkh_tune_decode_chunk(0)
