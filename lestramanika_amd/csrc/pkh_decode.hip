@@ -26,8 +26,9 @@
 // skipped on almost every tile.  At the end the row groups of a wave are
 // merged with row_ror DPP and the gfx950 permlane16/32 swaps, waves through
 // LDS, and the workgroup's (m, l, o) is either normalised into the output
-// (single-chunk sequences) or written as a split-K partial for the combine
-// kernel.
+// (single-chunk sequences) or written as a split-K partial; the last work
+// item of a (sequence, KV head) to finish merges the partials in the same
+// launch.
 //
 // RoPE and append.  Every workgroup rotates its own G query heads from the
 // host-computed table row `pos` (the same sin/cos bits as the reference's
