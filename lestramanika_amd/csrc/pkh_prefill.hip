@@ -8,22 +8,23 @@
 // cache ends up holding the same rows.  That is what is computed here, in
 // two launches on the caller's stream:
 //
-// prefill_stage  one workgroup per (tile of kKT rows, KV head).  New rows
-//                (p >= pos0) get k rotated in fp32 with the reference's
-//                contraction, and k_rot / v are appended to the cache in its
-//                element type; rows below pos0 are read back from the cache.
-//                Every row is also written, as fp16, into a tile buffer laid
-//                out exactly as the attention kernel keeps it in LDS:
-//                K as [key][D + kKPad] and V transposed as [d][kKT + kVPad].
-//                Rows past the last position are zero.
+// prefill_stage  one workgroup per (tile of KT rows, KV head); KT = 64 keys
+//                (32 for head_dim 256).  New rows (p >= pos0) get k rotated
+//                in fp32 with the reference's contraction, and k_rot / v are
+//                appended to the cache in its element type; rows below pos0
+//                are read back from the cache.  Every row is also written,
+//                as fp16, into a tile buffer laid out exactly as the
+//                attention kernel keeps it in LDS: K as [key][D + kKPad] and
+//                V transposed as [d][KT + kVPad].  Rows past the last
+//                position are zero.
 //
 // prefill_attn   one workgroup per (block of query positions, KV head),
 //                dispatched longest-first, with blockIdx % HK == KV head so
 //                that on an 8-XCD part each XCD's L2 holds one head's tiles.
-//                The 4 waves hold 128 query columns: column c is head
-//                c % G of the group at token c / G, so the G heads that share
-//                a KV head share every K/V tile.  Each wave computes
-//                S^T = K Q^T and O^T += V^T P^T with
+//                128 query columns per workgroup: column c is head c % G of
+//                the group at token c / G, so the G heads that share a KV
+//                head share every K/V tile.  Each wave holds 32 columns and
+//                computes S^T = K Q^T and O^T += V^T P^T with
 //                v_mfma_f32_32x32x16_f16: keeping the query index on the lane
 //                makes the softmax statistics per-lane scalars, and the
 //                S^T accumulator registers are, converted to fp16, exactly
@@ -31,8 +32,13 @@
 //                step are taken in the order the accumulator holds them
 //                (the V^T reads use the same order).  Softmax runs in fp32,
 //                in log2 units (q is pre-scaled by log2(e)/sqrt(D)), with a
-//                lazily rescaled running maximum.  Tiles are double-buffered
-//                in LDS with a register prefetch one tile ahead.
+//                lazily rescaled running maximum.
+//                Two groups of 4 waves (one wave of each per SIMD) split the
+//                key tiles by parity and alternate phases, so that while one
+//                group's waves issue MFMAs the other's run the softmax; the
+//                groups' (m, l, o) are merged at the end.  Tiles reach LDS
+//                through gfx950 direct loads (global_load_lds_dwordx4) into
+//                4-slot K and V rings, two phases ahead of use.
 
 #include "pkh_internal.h"
 
@@ -46,24 +52,22 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kKT = 64;         // keys per tile
 constexpr int kKPad = 8;        // fp16 padding per K row (conflict-free ds_read_b128)
 constexpr int kVPad = 4;        // fp16 padding per V^T row (conflict-free ds_read_b64)
-constexpr int kThreads = 256;   // 4 waves
-constexpr int kCols = 128;      // query columns per workgroup (32 per wave)
+constexpr int kThreads = 256;   // staging kernel: 4 waves
 constexpr float kTau = 8.0f;    // lazy-rescale threshold, log2 units
 
 constexpr int rope_half_of(int D) { return D / 2 < 64 ? D / 2 : 64; }
 
-// One staged tile of one KV head: K rows then V^T rows, fp16.
+// One staged tile of one KV head: KT keys' K rows then V^T rows, fp16.
 template <int D>
 struct Tile {
+    static constexpr int KT = D >= 256 ? 32 : 64;     // keys per tile
     static constexpr int KS = D + kKPad;              // K row stride
     static constexpr int VROWS = D < 32 ? 32 : D;     // V^T rows, zero-padded to a 32-row block
-    static constexpr int VS = kKT + kVPad;            // V^T row stride
-    static constexpr int K_ELEMS = kKT * KS;
+    static constexpr int VS = KT + kVPad;             // V^T row stride
+    static constexpr int K_ELEMS = KT * KS;
     static constexpr int V_ELEMS = VROWS * VS;
     static constexpr int ELEMS = K_ELEMS + V_ELEMS;
     static constexpr int BYTES = ELEMS * 2;
@@ -124,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void prefill_stage(StageParams P) {
     constexpr int NI = NP + NL;
     constexpr int TPR = NI < 16 ? NI : 16;    // threads per row
     constexpr int RPP = kThreads / TPR;       // rows per pass
-    __shared__ __attribute__((aligned(16))) _Float16 sv[kKT][D + 4];   // 8-byte aligned rows
+    __shared__ __attribute__((aligned(16))) _Float16 sv[TL::KT][D + 4];   // 8-byte aligned rows
 
     const int tid = threadIdx.x;
     const int j = blockIdx.x, g = blockIdx.y;
@@ -133,8 +137,8 @@ __global__ __launch_bounds__(kThreads) void prefill_stage(StageParams P) {
     CT* kc = static_cast<CT*>(P.k_layer) + (size_t)g * P.stride_head;
     CT* vc = static_cast<CT*>(P.v_layer) + (size_t)g * P.stride_head;
 
-    for (int r = tid / TPR; r < kKT; r += RPP) {
-        const int p = j * kKT + r;
+    for (int r = tid / TPR; r < TL::KT; r += RPP) {
+        const int p = j * TL::KT + r;
         for (int it = tid % TPR; it < NI; it += TPR) {
             const bool pair = it < NP;
             const int d0 = pair ? 4 * it : 2 * HALF + 4 * (it - NP);
@@ -185,8 +189,8 @@ __global__ __launch_bounds__(kThreads) void prefill_stage(StageParams P) {
     }
     __syncthreads();
     // V^T rows, 8 keys per store (two 8-byte halves: rows are 8-byte aligned).
-    for (int u = tid; u < TL::VROWS * (kKT / 8); u += kThreads) {
-        const int d = u / (kKT / 8), c8 = u % (kKT / 8);
+    for (int u = tid; u < TL::VROWS * (TL::KT / 8); u += kThreads) {
+        const int d = u / (TL::KT / 8), c8 = u % (TL::KT / 8);
         h4 lo, hi;
         for (int i = 0; i < 4; i++) {
             lo[i] = d < D ? sv[8 * c8 + i][d] : (_Float16)0.0f;
@@ -222,73 +226,93 @@ __device__ __forceinline__ float sum_halves(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// A tile moves HBM/L2 -> registers -> LDS in 16-byte chunks; the register
-// copy of the next tile is held across the current tile's compute.
-template <int D>
-struct TileRegs {
-    static constexpr int CH = Tile<D>::BYTES / 16;     // chunks per tile
-    static constexpr int FULL = CH / kThreads;         // chunks every thread moves
-    static constexpr bool TAIL = CH % kThreads != 0;   // one more for the first threads
-    u32x4 r[FULL + 1];
+// Copy `bytes` (a multiple of 16) from global memory to LDS with the gfx950
+// direct loads: each instruction moves 1 KB, lane l's 16 bytes landing at
+// dst + 16*l.  Instructions are dealt round-robin to the waves; the data is
+// visible to the workgroup after s_waitcnt vmcnt(0) and a barrier.
+template <int BYTES, int WAVES>
+__device__ __forceinline__ void copy_to_lds(_Float16* dst, const _Float16* src, int wave, int lane) {
+    constexpr int CH = BYTES / 16;                 // 16-byte chunks
+    constexpr int NI = (CH + 63) / 64;             // wave instructions
+#pragma unroll
+    for (int i = wave; i < NI; i += WAVES) {
+        const int c = 64 * i + lane;
+        if (NI * 64 == CH || c < CH)
+            __builtin_amdgcn_global_load_lds(
+                reinterpret_cast<const void*>(reinterpret_cast<const char*>(src) + 16 * c),
+                (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(dst) + 1024 * i),
+                16, 0, 0);
+    }
+}
 
-    // Fold expressions keep every index a constant, so r[] stays in VGPRs.
-    template <int... I>
-    __device__ __forceinline__ void load_full(const u32x4* src, int tid,
-                                              std::integer_sequence<int, I...>) {
-        ((r[I] = src[tid + kThreads * I]), ...);
-    }
-    template <int... I>
-    __device__ __forceinline__ void store_full(u32x4* dst, int tid,
-                                               std::integer_sequence<int, I...>) const {
-        ((dst[tid + kThreads * I] = r[I]), ...);
-    }
-    __device__ __forceinline__ void load(const u32x4* src, int tid) {
-        load_full(src, tid, std::make_integer_sequence<int, FULL>{});
-        if constexpr (TAIL) {
-            if (tid + kThreads * FULL < CH) r[FULL] = src[tid + kThreads * FULL];
-        }
-    }
-    __device__ __forceinline__ void store(_Float16* dst, int tid) const {
-        u32x4* d = reinterpret_cast<u32x4*>(dst);
-        store_full(d, tid, std::make_integer_sequence<int, FULL>{});
-        if constexpr (TAIL) {
-            if (tid + kThreads * FULL < CH) d[tid + kThreads * FULL] = r[FULL];
-        }
-    }
-};
+// The attention workgroup: two groups of 4 waves, one wave of each group on
+// every SIMD.  Both groups hold the same 128 query columns (32 per wave);
+// group 0 takes the even key tiles and group 1 the odd ones (split-K), and
+// the groups alternate phases: while one group's waves run MFMAs the other
+// group's run the softmax on the VALU.
+// head_dim 256 needs the whole register file for one wave per SIMD: one
+// group of 4 waves that runs each tile's QK, softmax and P.V in turn.
+template <int D> struct Groups { static constexpr int N = D >= 256 ? 1 : 2; };
+constexpr int kSlots = 4;        // K ring and V ring depth
+constexpr int kCols = 128;       // query columns per workgroup
 
 template <int D, int G>
-__global__ __launch_bounds__(kThreads, D >= 256 ? 1 : 2) void prefill_attn(AttnParams P) {
+__global__ __launch_bounds__(256 * Groups<D>::N)
+__attribute__((amdgpu_waves_per_eu(Groups<D>::N, Groups<D>::N)))
+void prefill_attn(AttnParams P) {
     using TL = Tile<D>;
+    constexpr int NG = Groups<D>::N;
+    constexpr int kAttnWaves = 4 * NG;
+    constexpr int KT = TL::KT;
     constexpr int HALF = rope_half_of(D);
-    constexpr int NKS = D / 16;             // k-steps of S^T = K Q^T
-    constexpr int NDB = TL::VROWS / 32;     // 32-row blocks of O^T
-    constexpr int NKB = kKT / 32;           // 32-key blocks per tile
-    constexpr int BM = kCols / G;           // query positions per workgroup
-    constexpr int CH = TL::BYTES / 16;
-    __shared__ __attribute__((aligned(16))) _Float16 lds[2][TL::ELEMS];
+    constexpr int BM = kCols / G;                 // query positions per workgroup
+    constexpr int NKS = D / 16;                   // k-steps of S^T = K Q^T
+    constexpr int NDB = TL::VROWS / 32;           // 32-row blocks of O^T
+    constexpr int NKB = KT / 32;                  // 32-key blocks per tile
+    constexpr int NT = KT / 16;                   // 16-key steps per tile
+    // Distinct LDS objects per ring slot (not one indexed array), so the
+    // compiler can tell a slot being filled by a direct load from the slots
+    // being read, and does not wait for the load before those reads.
+    __shared__ __attribute__((aligned(16))) _Float16 k0[TL::K_ELEMS], k1[TL::K_ELEMS],
+        k2[TL::K_ELEMS], k3[TL::K_ELEMS];
+    __shared__ __attribute__((aligned(16))) _Float16 v0[TL::V_ELEMS], v1[TL::V_ELEMS],
+        v2[TL::V_ELEMS], v3[TL::V_ELEMS];
+    _Float16* const kslot[kSlots] = {k0, k1, k2, k3};
+    _Float16* const vslot[kSlots] = {v0, v1, v2, v3};
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, hh = lane >> 5, l32 = lane & 31;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = w >> 2, sub = w & 3;
     const int g = blockIdx.x % P.HK;
-    const int qb = P.nqb - 1 - (int)(blockIdx.x / P.HK);
-    const int col = 32 * w + l32;
+    const int qb = P.nqb - 1 - (int)(blockIdx.x / P.HK);      // longest first
+    const int qmin_wg = P.pos0 + qb * BM;
+    const int qmax = P.pos0 + min(qb * BM + BM - 1, P.n - 1);
+    const int ntile = qmax / KT + 1;
+
+    const _Float16* src = P.tiles + (size_t)g * P.T * TL::ELEMS;
+    auto load_k = [&](_Float16* dst, int t) __attribute__((always_inline)) {
+        copy_to_lds<TL::K_ELEMS * 2, kAttnWaves>(dst, src + (size_t)t * TL::ELEMS, w, lane);
+    };
+    auto load_v = [&](_Float16* dst, int t) __attribute__((always_inline)) {
+        copy_to_lds<TL::V_ELEMS * 2, kAttnWaves>(dst, src + (size_t)t * TL::ELEMS + TL::K_ELEMS, w, lane);
+    };
+    load_k(k0, 0);
+    if (ntile > 1) load_k(k1, 1);
+    if constexpr (NG == 1) {
+        load_v(v0, 0);
+        if (ntile > 1) load_v(v1, 1);
+    }
+
+    // ---- q: load, rotate (same contraction as the reference), scale, fp16.
+    // Lane (l32, hh) of wave `sub` holds column 32*sub + l32 and, for k-step
+    // ks, elements d = 16ks + 8hh + [0, 8).
+    const int col = 32 * sub + l32;
     const int ti = qb * BM + col / G;
     const bool valid = ti < P.n;
     const int tic = valid ? ti : P.n - 1;
     const int h = g * G + col % G;
     const int qpos = P.pos0 + tic;
-    const int qmin_w = P.pos0 + min(qb * BM + (32 * w) / G, P.n - 1);
-    const int qmax = P.pos0 + min(qb * BM + BM - 1, P.n - 1);
-    const int ntile = qmax / kKT + 1;
-
-    const u32x4* src = reinterpret_cast<const u32x4*>(P.tiles + (size_t)g * P.T * TL::ELEMS);
-    TileRegs<D> pre;
-    pre.load(src, tid);
-
-    // ---- q: load, rotate (same contraction as the reference), scale, fp16.
-    // Lane (l32, hh) holds, for k-step ks, elements d = 16ks + 8hh + [0, 8).
     h8 qt[NKS];
     {
         const float* qrow = P.q + ((size_t)tic * P.H + h) * D;
@@ -308,20 +332,20 @@ __global__ __launch_bounds__(kThreads, D >= 256 ? 1 : 2) void prefill_attn(AttnP
             constexpr int KH = HALF / 16;
 #pragma unroll
             for (int ks = 0; ks < KH; ks++) {
-                float s[8], c[8];
+                float sn[8], cs[8];
                 const float4 s0 = *reinterpret_cast<const float4*>(srow + 16 * ks + 8 * hh);
                 const float4 s1 = *reinterpret_cast<const float4*>(srow + 16 * ks + 8 * hh + 4);
                 const float4 c0 = *reinterpret_cast<const float4*>(crow + 16 * ks + 8 * hh);
                 const float4 c1 = *reinterpret_cast<const float4*>(crow + 16 * ks + 8 * hh + 4);
-                s[0] = s0.x; s[1] = s0.y; s[2] = s0.z; s[3] = s0.w;
-                s[4] = s1.x; s[5] = s1.y; s[6] = s1.z; s[7] = s1.w;
-                c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w;
-                c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
+                sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w;
+                sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
+                cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w;
+                cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const float a = x[ks][e], b = x[ks + KH][e];
-                    y[ks][e] = fmaf(c[e], a, -(s[e] * b));
-                    y[ks + KH][e] = fmaf(s[e], a, c[e] * b);
+                    y[ks][e] = fmaf(cs[e], a, -(sn[e] * b));
+                    y[ks + KH][e] = fmaf(sn[e], a, cs[e] * b);
                 }
             }
 #pragma unroll
@@ -335,14 +359,14 @@ __global__ __launch_bounds__(kThreads, D >= 256 ? 1 : 2) void prefill_attn(AttnP
             const float4 s1 = *reinterpret_cast<const float4*>(srow + 4);
             const float4 c0 = *reinterpret_cast<const float4*>(crow);
             const float4 c1 = *reinterpret_cast<const float4*>(crow + 4);
-            const float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-            const float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+            const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const float other = __shfl_xor(x[0][e], 32);
                 const float a = hh ? other : x[0][e];    // element d
                 const float b = hh ? x[0][e] : other;    // element d + 8
-                y[0][e] = hh ? fmaf(s[e], a, c[e] * b) : fmaf(c[e], a, -(s[e] * b));
+                y[0][e] = hh ? fmaf(sn[e], a, cs[e] * b) : fmaf(cs[e], a, -(sn[e] * b));
             }
         }
 #pragma unroll
@@ -354,51 +378,65 @@ __global__ __launch_bounds__(kThreads, D >= 256 ? 1 : 2) void prefill_attn(AttnP
         }
     }
 
-    pre.store(lds[0], tid);
-    if (ntile > 1) pre.load(src + CH, tid);
-    __syncthreads();
-
     f32x16 acc[NDB];
 #pragma unroll
     for (int b = 0; b < NDB; b++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[b][r] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
+    f32x16 S[NKB];                 // scores of this wave's current tile
+    h8 pt[NT];                     // its fp16 weights, B operands of P^T
 
-    for (int j = 0; j < ntile; j++) {
-        const _Float16* sk = lds[j & 1];
-        const _Float16* sv = sk + TL::K_ELEMS;
-
-        // S^T block kb: rows = keys kb*32 + 8(r/4) + 4hh + r%4, column = l32.
-        f32x16 s[NKB];
+    // S^T block kb: rows = keys kb*32 + 8(r/4) + 4hh + r%4 of the tile,
+    // column = l32.
+    auto qk = [&](const _Float16* sk) __attribute__((always_inline)) {
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) s[kb][r] = 0.0f;
+            for (int r = 0; r < 16; r++) S[kb][r] = 0.0f;
             const _Float16* krow = sk + (kb * 32 + l32) * TL::KS + 8 * hh;
 #pragma unroll
             for (int ks = 0; ks < NKS; ks++) {
                 const h8 a = *reinterpret_cast<const h8*>(krow + 16 * ks);
-                s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qt[ks], s[kb], 0, 0, 0);
+                S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qt[ks], S[kb], 0, 0, 0);
             }
         }
-
-        const int kbase = j * kKT;
-        if (kbase + kKT - 1 > qmin_w) {   // causal mask, only near the diagonal
+    };
+    // O^T block b += V^T[32b + l32][keys of step t] * P^T[t].  The k index
+    // 8hh + c of step t = (kb, tt) is key kb*32 + 16tt + 4hh + c for c < 4 and
+    // kb*32 + 16tt + 8 + 4hh + (c - 4) for c >= 4: the order in which the S^T
+    // accumulator holds them.
+    auto pv = [&](const _Float16* sv) __attribute__((always_inline)) {
+#pragma unroll
+        for (int b = 0; b < NDB; b++) {
+            const _Float16* vrow = sv + (32 * b + l32) * TL::VS + 4 * hh;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const h4 lo = *reinterpret_cast<const h4*>(vrow + 16 * t);
+                const h4 hi = *reinterpret_cast<const h4*>(vrow + 16 * t + 8);
+                const h8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pt[t], acc[b], 0, 0, 0);
+            }
+        }
+    };
+    // Online softmax of tile t's scores: causal mask near the diagonal, lazy
+    // running max (the accumulator is rescaled only when the max grows by
+    // more than kTau), exp2, row sums of the fp16 weights as P^T uses them.
+    auto softmax = [&](int t) __attribute__((always_inline)) {
+        if (t * KT + KT - 1 > qmin_wg) {
 #pragma unroll
             for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int key = kbase + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
-                    if (key > qpos) s[kb][r] = -INFINITY;
+                    const int key = t * KT + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    if (key > qpos) S[kb][r] = -INFINITY;
                 }
         }
-
         float mt = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[kb][r]);
+            for (int r = 0; r < 16; r++) mt = fmaxf(mt, S[kb][r]);
         mt = max_halves(mt);
         const bool need = mt > m_run + kTau;
         if (__builtin_amdgcn_ballot_w64(need)) {
@@ -411,58 +449,149 @@ __global__ __launch_bounds__(kThreads, D >= 256 ? 1 : 2) void prefill_attn(AttnP
             l_run *= alpha;
             m_run = mn;
         }
-
-        h8 pt[kKT / 16];
+        // A group's first tiles can be fully masked for a column (the odd
+        // group starts at keys KT..2KT-1): its max is then still -inf and its
+        // weights are exp2(-inf - 0) = 0 rather than exp2(-inf + inf).
+        const float msub = m_run == -INFINITY ? 0.0f : m_run;
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
-        for (int t = 0; t < kKT / 16; t++) {
+        for (int t2 = 0; t2 < NT; t2++) {
             h8 v;
 #pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const float p = __builtin_amdgcn_exp2f(s[t >> 1][8 * (t & 1) + c] - m_run);
-                l_run += p;
-                v[c] = (_Float16)p;
-            }
-            pt[t] = v;
-        }
-
-        // O^T block b += V^T[32b + l32][keys of step t] * P^T[step t].  The
-        // k index 8hh + c of step t = (kb, tt) is key kb*32 + 16tt + 4hh + c
-        // for c < 4 and kb*32 + 16tt + 8 + 4hh + (c - 4) for c >= 4: the
-        // order in which the S^T accumulator holds them.
+            for (int c = 0; c < 8; c++)
+                v[c] = (_Float16)__builtin_amdgcn_exp2f(S[t2 >> 1][8 * (t2 & 1) + c] - msub);
+            pt[t2] = v;
 #pragma unroll
-        for (int b = 0; b < NDB; b++) {
-            const _Float16* vrow = sv + (32 * b + l32) * TL::VS + 4 * hh;
-#pragma unroll
-            for (int t = 0; t < kKT / 16; t++) {
-                const h4 lo = *reinterpret_cast<const h4*>(vrow + 16 * t);
-                const h4 hi = *reinterpret_cast<const h4*>(vrow + 16 * t + 8);
-                const h8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pt[t], acc[b], 0, 0, 0);
+            for (int c = 0; c < 8; c += 2) {
+                const h2 p2 = {v[c], v[c + 1]};
+                l_run = __builtin_amdgcn_fdot2(p2, one, l_run, false);
             }
         }
+    };
 
-        if (j + 1 < ntile) {
-            pre.store(lds[(j + 1) & 1], tid);
-            if (j + 2 < ntile) pre.load(src + (size_t)(j + 2) * CH, tid);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    // Phase p (p = 0 .. ntile + 1): the group p % 2 runs MFMAs -- P.V of
+    // tile p - 2 (its previous tile) and QK of tile p -- while the other
+    // group runs tile p - 1's softmax.  Slots: K(t) in kslot[t % 4], V(t) in
+    // vslot[t % 4].  Phase p loads K(p + 2) and V(p), needed two phases
+    // later; their slots were last read in phase p - 2.  Each group runs its
+    // own straight-line phase sequence (group 0: M V M V ..., group 1:
+    // V M V M ...), both with one barrier per phase, unrolled by four so
+    // every slot is a fixed LDS object.
+    const int nphase = NG == 2 ? ntile + 2 : ntile;
+    auto dma = [&](int p, int R) __attribute__((always_inline)) {
+        if constexpr (NG == 2) {
+            if (p + 2 < ntile) load_k(kslot[(R + 2) % kSlots], p + 2);
+            if (p < ntile) load_v(vslot[R], p);
+        } else {
+            if (p + 2 < ntile) {
+                load_k(kslot[(R + 2) % kSlots], p + 2);
+                load_v(vslot[(R + 2) % kSlots], p + 2);
+            }
         }
+    };
+    auto sync = [&]() __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+    };
+    auto mphase = [&](int p, int R) __attribute__((always_inline)) {
+        if (p >= 2 && p - 2 < ntile) pv(vslot[(R + 2) % kSlots]);
+        __builtin_amdgcn_sched_barrier(0);   // P.V's weights die before QK's scores are born
+        if (p < ntile) qk(kslot[R]);
+    };
+    auto vphase = [&](int p) __attribute__((always_inline)) {
+        if (p >= 1 && p - 1 < ntile) softmax(p - 1);
+    };
+    if constexpr (NG == 2) {
+        if (grp == 0) {
+            for (int p = 0; p < nphase; p += 4) {
+                dma(p, 0); mphase(p, 0); sync();
+                if (p + 1 >= nphase) break;
+                dma(p + 1, 1); vphase(p + 1); sync();
+                if (p + 2 >= nphase) break;
+                dma(p + 2, 2); mphase(p + 2, 2); sync();
+                if (p + 3 >= nphase) break;
+                dma(p + 3, 3); vphase(p + 3); sync();
+            }
+        } else {
+            for (int p = 0; p < nphase; p += 4) {
+                dma(p, 0); vphase(p); sync();
+                if (p + 1 >= nphase) break;
+                dma(p + 1, 1); mphase(p + 1, 1); sync();
+                if (p + 2 >= nphase) break;
+                dma(p + 2, 2); vphase(p + 2); sync();
+                if (p + 3 >= nphase) break;
+                dma(p + 3, 3); mphase(p + 3, 3); sync();
+            }
+        }
+    } else {
+        // One group: phase p runs tile p start to finish.
+        auto whole = [&](int p, int R) __attribute__((always_inline)) {
+            dma(p, R);
+            if (p < ntile) {
+                qk(kslot[R]);
+                softmax(p);
+                pv(vslot[R]);
+            }
+            sync();
+        };
+        for (int p = 0; p < nphase; p += 4) {
+            whole(p, 0);
+            if (p + 1 < nphase) whole(p + 1, 1);
+            if (p + 2 < nphase) whole(p + 2, 2);
+            if (p + 3 < nphase) whole(p + 3, 3);
+        }
     }
 
-    // ---- normalise and write: lane holds O^T[d][l32] for
-    // d = 32b + 8(r/4) + 4hh + r%4.
-    const float inv = 1.0f / sum_halves(l_run);
-    if (valid) {
-        float* orow = P.out + ((size_t)ti * P.H + h) * D;
+    // ---- merge the groups' (m, l, o) and write O[d][column] for
+    // d = 32b + 8(r/4) + 4hh + r%4.  Group 1 hands its state to group 0
+    // through a dedicated LDS buffer, one 32-row block of O^T at a time.
+    __shared__ float xm[NG == 2 ? 4 * 2 * 64 : 1];
+    __shared__ float xo[NG == 2 ? 4 * 16 * 64 : 1];
+    float fa = 1.0f, fb = 0.0f, inv;
+    if constexpr (NG == 2) {
+        if (grp == 1) {
+            xm[(sub * 2 + 0) * 64 + lane] = m_run;
+            xm[(sub * 2 + 1) * 64 + lane] = l_run;
+        }
+        __syncthreads();
+        const float mb = xm[(sub * 2 + 0) * 64 + lane];
+        const float lb = xm[(sub * 2 + 1) * 64 + lane];
+        const float M = fmaxf(m_run, mb);
+        fa = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
+        fb = mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb - M);
+        inv = 1.0f / sum_halves(l_run * fa + lb * fb);
+    } else {
+        inv = 1.0f / sum_halves(l_run);
+    }
+    float* orow = P.out + ((size_t)ti * P.H + h) * D;
 #pragma unroll
-        for (int b = 0; b < NDB; b++)
+    for (int b = 0; b < NDB; b++) {
+        if constexpr (NG == 2) {
+            if (grp == 1) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) xo[(sub * 16 + r) * 64 + lane] = acc[b][r];
+            }
+            __syncthreads();
+        }
+        if (grp == 0 && valid) {
 #pragma unroll
             for (int r4 = 0; r4 < 4; r4++) {
                 const int d = 32 * b + 8 * r4 + 4 * hh;
-                if (d < D)
-                    *reinterpret_cast<float4*>(orow + d) =
-                        make_float4(acc[b][4 * r4] * inv, acc[b][4 * r4 + 1] * inv,
-                                    acc[b][4 * r4 + 2] * inv, acc[b][4 * r4 + 3] * inv);
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int r = 4 * r4 + e;
+                    const float ob = NG == 2 ? xo[(sub * 16 + r) * 64 + lane] : 0.0f;
+                    o[e] = (acc[b][r] * fa + ob * fb) * inv;
+                }
+                if (d < D) *reinterpret_cast<float4*>(orow + d) = make_float4(o[0], o[1], o[2], o[3]);
             }
+        }
+        if constexpr (NG == 2) __syncthreads();
     }
 }
 
@@ -472,7 +601,7 @@ template <int D, int G, typename CT>
 int launch_dg(const PrefillArgs& a, hipStream_t st) {
     using TL = Tile<D>;
     const long long rows = (long long)a.pos0 + a.n_tokens;
-    const int T = (int)((rows + kKT - 1) / kKT);
+    const int T = (int)((rows + TL::KT - 1) / TL::KT);
     const int HK = a.n_kv_heads;
     void* tiles = nullptr;
     int rc = tiles_get((size_t)HK * T * TL::BYTES, &tiles);
@@ -511,7 +640,7 @@ int launch_dg(const PrefillArgs& a, hipStream_t st) {
     A.HK = HK;
     A.nqb = (a.n_tokens + BM - 1) / BM;
     A.qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
-    hipLaunchKernelGGL((prefill_attn<D, G>), dim3(A.nqb * HK), dim3(kThreads), 0, st, A);
+    hipLaunchKernelGGL((prefill_attn<D, G>), dim3(A.nqb * HK), dim3(256 * Groups<D>::N), 0, st, A);
     PKH_HIP(hipGetLastError());
     return PKH_OK;
 }
