@@ -48,6 +48,7 @@ namespace {
 
 constexpr float kTau = 8.0f;   // lazy-rescale threshold (log2 units)
 constexpr int kCoherent = 16;  // buffer cache policy: sc1, device-coherent access
+constexpr int kStream = 3;     // buffer cache policy: sc0 | nt, read-once KV stream
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
@@ -321,9 +322,9 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
 #pragma unroll
         for (int i = 0; i < NLD; i++) {
             kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                        krs, off + (unsigned)(S * i * sizeof(KT)), 0, 0));
+                        krs, off + (unsigned)(S * i * sizeof(KT)), 0, kStream));
             vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                        vrs, off + (unsigned)(S * i * sizeof(KT)), 0, 0));
+                        vrs, off + (unsigned)(S * i * sizeof(KT)), 0, kStream));
         }
     };
     auto use = [&](int t, const uint4 (&kr)[NLD], const uint4 (&vr)[NLD]) {
@@ -664,6 +665,13 @@ int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
         const long long target_items = 160;
         chunk = (total_rows * n_kv_heads + target_items - 1) / target_items;
         if (chunk < 2LL * tile) chunk = 2LL * tile;
+        // Large batches (many sequence x head pairs) finish their merges at
+        // different times, hidden behind other items' streaming, so smaller
+        // items balance better: measured on 16 sequences of 4K-32K rows,
+        // 768-1536-row items stream at 72% of HBM peak against 58% for
+        // 13K-row items.
+        const long long max_chunk = 1024;
+        if (chunk > max_chunk) chunk = max_chunk;
     }
     chunk = (chunk + tile - 1) / tile * tile;
     if (chunk > (long long)max_attend) chunk = ((long long)max_attend + tile - 1) / tile * tile;
