@@ -8,8 +8,8 @@
 // cache ends up holding the same rows.  That is what is computed here, in
 // two launches on the caller's stream:
 //
-// prefill_stage  one workgroup per (tile of KT rows, KV head); KT = 64 keys
-//                (32 for head_dim 256).  New rows (p >= pos0) get k rotated
+// prefill_stage  one workgroup per (32 rows of a tile of KT rows, KV head);
+//                KT = 64 keys (32 for head_dim 256).  New rows (p >= pos0) get k rotated
 //                in fp32 with the reference's contraction, and k_rot / v are
 //                appended to the cache in its element type; rows below pos0
 //                are read back from the cache.  Every row is also written,
@@ -119,6 +119,10 @@ struct StageParams {
     _Float16* tiles;            // [HK][T][Tile::ELEMS]
 };
 
+// Rows of one tile that one staging workgroup covers (two workgroups per
+// 64-key tile: 512 workgroups for a 2048-row, 8-head layer).
+template <int D> struct StageRows { static constexpr int N = Tile<D>::KT < 32 ? Tile<D>::KT : 32; };
+
 template <int D, typename CT>
 __global__ __launch_bounds__(kThreads) void prefill_stage(StageParams P) {
     using TL = Tile<D>;
@@ -128,75 +132,110 @@ __global__ __launch_bounds__(kThreads) void prefill_stage(StageParams P) {
     constexpr int NI = NP + NL;
     constexpr int TPR = NI < 16 ? NI : 16;    // threads per row
     constexpr int RPP = kThreads / TPR;       // rows per pass
-    __shared__ __attribute__((aligned(16))) _Float16 sv[TL::KT][D + 4];   // 8-byte aligned rows
+    constexpr int RW = StageRows<D>::N;       // rows of this workgroup
+    constexpr int NPASS = RW > RPP ? RW / RPP : 1;
+    constexpr int NIT = (NI + TPR - 1) / TPR;
+    constexpr int NU = NPASS * NIT;           // (row, group) items per thread
+    static_assert(RW % RPP == 0 || RPP > RW, "rows split evenly over passes");
+    __shared__ __attribute__((aligned(16))) _Float16 sv[RW][D + 4];   // 8-byte aligned rows
 
     const int tid = threadIdx.x;
-    const int j = blockIdx.x, g = blockIdx.y;
+    constexpr int SPLIT = TL::KT / RW;
+    const int j = blockIdx.x / SPLIT, r0 = (blockIdx.x % SPLIT) * RW, g = blockIdx.y;
     _Float16* tk = P.tiles + ((size_t)g * P.T + j) * TL::ELEMS;
     _Float16* tv = tk + TL::K_ELEMS;
     CT* kc = static_cast<CT*>(P.k_layer) + (size_t)g * P.stride_head;
     CT* vc = static_cast<CT*>(P.v_layer) + (size_t)g * P.stride_head;
 
-    for (int r = tid / TPR; r < TL::KT; r += RPP) {
-        const int p = j * TL::KT + r;
-        for (int it = tid % TPR; it < NI; it += TPR) {
-            const bool pair = it < NP;
-            const int d0 = pair ? 4 * it : 2 * HALF + 4 * (it - NP);
-            float k0[4] = {0, 0, 0, 0}, k1[4] = {0, 0, 0, 0};
-            float v0[4] = {0, 0, 0, 0}, v1[4] = {0, 0, 0, 0};
-            if (p < P.pos0) {
-                // Earlier context: already rotated in the cache.
-                const size_t row = (size_t)p * P.stride_pos;
-                load4(kc + row + d0, k0);
-                load4(vc + row + d0, v0);
-                if (pair) {
-                    load4(kc + row + d0 + HALF, k1);
-                    load4(vc + row + d0 + HALF, v1);
-                }
-            } else if (p < P.pos0 + P.n) {
-                const size_t src = ((size_t)(p - P.pos0) * P.HK + g) * D;
-                load4(P.k_new + src + d0, k0);
-                load4(P.v_new + src + d0, v0);
-                if (pair) {
-                    load4(P.k_new + src + d0 + HALF, k1);
-                    load4(P.v_new + src + d0 + HALF, v1);
-                    float s[4], c[4];
-                    load4(P.rope_sin + (size_t)p * P.half + d0, s);
-                    load4(P.rope_cos + (size_t)p * P.half + d0, c);
-                    for (int i = 0; i < 4; i++) {
-                        // src/pickle_fast.c:1917-1922 as compiled: x0' = c*x0 - s*x1
-                        // and x1' = s*x0 + c*x1, each one fused multiply-add.
-                        const float a = k0[i], b = k1[i];
-                        k0[i] = fmaf(c[i], a, -(s[i] * b));
-                        k1[i] = fmaf(s[i], a, c[i] * b);
-                    }
-                }
-                const size_t row = (size_t)p * P.stride_pos;
-                store4(kc + row + d0, k0);
-                store4(vc + row + d0, v0);
-                if (pair) {
-                    store4(kc + row + d0 + HALF, k1);
-                    store4(vc + row + d0 + HALF, v1);
-                }
-            }
-            *reinterpret_cast<h4*>(tk + r * TL::KS + d0) = to_h4(k0);
-            *reinterpret_cast<h4*>(&sv[r][d0]) = to_h4(v0);
+    // Item u = (pass, i): local row rl = tid / TPR + pass * RPP, 4-element
+    // group it = tid % TPR + i * TPR.  All of a thread's loads are issued
+    // before any of its stores (a store to the cache may alias an input, so
+    // the compiler could not hoist a later item's loads above it).
+    float k0[NU][4], k1[NU][4], v0[NU][4], v1[NU][4];
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        const int rl = tid / TPR + (u / NIT) * RPP, it = tid % TPR + (u % NIT) * TPR;
+        const int p = j * TL::KT + r0 + rl;
+        const bool pair = it < NP;
+        const int d0 = pair ? 4 * it : 2 * HALF + 4 * (it - NP);
+#pragma unroll
+        for (int i = 0; i < 4; i++) k0[u][i] = k1[u][i] = v0[u][i] = v1[u][i] = 0.0f;
+        if (rl >= RW || it >= NI) continue;
+        if (p < P.pos0) {
+            // Earlier context: already rotated in the cache.
+            const size_t row = (size_t)p * P.stride_pos;
+            load4(kc + row + d0, k0[u]);
+            load4(vc + row + d0, v0[u]);
             if (pair) {
-                *reinterpret_cast<h4*>(tk + r * TL::KS + d0 + HALF) = to_h4(k1);
-                *reinterpret_cast<h4*>(&sv[r][d0 + HALF]) = to_h4(v1);
+                load4(kc + row + d0 + HALF, k1[u]);
+                load4(vc + row + d0 + HALF, v1[u]);
+            }
+        } else if (p < P.pos0 + P.n) {
+            const size_t src = ((size_t)(p - P.pos0) * P.HK + g) * D;
+            load4(P.k_new + src + d0, k0[u]);
+            load4(P.v_new + src + d0, v0[u]);
+            if (pair) {
+                load4(P.k_new + src + d0 + HALF, k1[u]);
+                load4(P.v_new + src + d0 + HALF, v1[u]);
             }
         }
     }
+    float sn[NU][4], cs[NU][4];
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        const int rl = tid / TPR + (u / NIT) * RPP, it = tid % TPR + (u % NIT) * TPR;
+        const int p = j * TL::KT + r0 + rl;
+        if (rl < RW && it < NP && p >= P.pos0 && p < P.pos0 + P.n) {
+            load4(P.rope_sin + (size_t)p * P.half + 4 * it, sn[u]);
+            load4(P.rope_cos + (size_t)p * P.half + 4 * it, cs[u]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        const int rl = tid / TPR + (u / NIT) * RPP, it = tid % TPR + (u % NIT) * TPR;
+        if (rl >= RW || it >= NI) continue;
+        const int p = j * TL::KT + r0 + rl;
+        const bool pair = it < NP;
+        const int d0 = pair ? 4 * it : 2 * HALF + 4 * (it - NP);
+        if (p >= P.pos0 && p < P.pos0 + P.n) {
+            if (pair) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    // src/pickle_fast.c:1917-1922 as compiled: x0' = c*x0 - s*x1
+                    // and x1' = s*x0 + c*x1, each one fused multiply-add.
+                    const float a = k0[u][i], b = k1[u][i];
+                    k0[u][i] = fmaf(cs[u][i], a, -(sn[u][i] * b));
+                    k1[u][i] = fmaf(sn[u][i], a, cs[u][i] * b);
+                }
+            }
+            const size_t row = (size_t)p * P.stride_pos;
+            store4(kc + row + d0, k0[u]);
+            store4(vc + row + d0, v0[u]);
+            if (pair) {
+                store4(kc + row + d0 + HALF, k1[u]);
+                store4(vc + row + d0 + HALF, v1[u]);
+            }
+        }
+        const int r = r0 + rl;
+        *reinterpret_cast<h4*>(tk + r * TL::KS + d0) = to_h4(k0[u]);
+        *reinterpret_cast<h4*>(&sv[rl][d0]) = to_h4(v0[u]);
+        if (pair) {
+            *reinterpret_cast<h4*>(tk + r * TL::KS + d0 + HALF) = to_h4(k1[u]);
+            *reinterpret_cast<h4*>(&sv[rl][d0 + HALF]) = to_h4(v1[u]);
+        }
+    }
     __syncthreads();
-    // V^T rows, 8 keys per store (two 8-byte halves: rows are 8-byte aligned).
-    for (int u = tid; u < TL::VROWS * (TL::KT / 8); u += kThreads) {
-        const int d = u / (TL::KT / 8), c8 = u % (TL::KT / 8);
+    // V^T rows of this workgroup's keys, 8 keys per store (two 8-byte
+    // halves: rows are 8-byte aligned).
+    for (int u = tid; u < TL::VROWS * (RW / 8); u += kThreads) {
+        const int d = u / (RW / 8), c8 = u % (RW / 8);
         h4 lo, hi;
+#pragma unroll
         for (int i = 0; i < 4; i++) {
             lo[i] = d < D ? sv[8 * c8 + i][d] : (_Float16)0.0f;
             hi[i] = d < D ? sv[8 * c8 + 4 + i][d] : (_Float16)0.0f;
         }
-        _Float16* dst = tv + d * TL::VS + 8 * c8;
+        _Float16* dst = tv + d * TL::VS + r0 + 8 * c8;
         *reinterpret_cast<h4*>(dst) = lo;
         *reinterpret_cast<h4*>(dst + 4) = hi;
     }
@@ -250,6 +289,44 @@ __device__ __forceinline__ void copy_to_lds(_Float16* dst, const _Float16* src, 
 // group 0 takes the even key tiles and group 1 the odd ones (split-K), and
 // the groups alternate phases: while one group's waves run MFMAs the other
 // group's run the softmax on the VALU.
+// s_waitcnt vmcnt(n) for a wave-uniform n < 16 (lgkmcnt and expcnt are not
+// waited on): returns once at most n of this wave's vector-memory operations
+// are outstanding.  Loads complete in order, so this waits for everything
+// issued before the last n.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+#define PKH_VM(N) case N: __builtin_amdgcn_s_waitcnt(0xF70 | N); break;
+        PKH_VM(0) PKH_VM(1) PKH_VM(2) PKH_VM(3) PKH_VM(4) PKH_VM(5) PKH_VM(6) PKH_VM(7)
+        PKH_VM(8) PKH_VM(9) PKH_VM(10) PKH_VM(11) PKH_VM(12) PKH_VM(13) PKH_VM(14)
+#undef PKH_VM
+        default: __builtin_amdgcn_s_waitcnt(0xF70); break;
+    }
+}
+
+// Direct-load instructions a wave issues for one copy_to_lds<BYTES, WAVES>.
+template <int BYTES, int WAVES>
+__device__ __forceinline__ int copy_count(int wave) {
+    constexpr int NI = (BYTES / 16 + 63) / 64;
+    return (NI - wave + WAVES - 1) / WAVES;
+}
+
+// Issue order for a run of N MFMAs that each consume one LDS fragment: the
+// first kAhead fragment reads, then one MFMA and the next read in turn, so
+// every MFMA finds its operand kAhead reads back instead of waiting on its
+// own read.
+constexpr int kAhead = 8;
+template <int N>
+__device__ __forceinline__ void pipeline_order() {
+    constexpr int A = N < kAhead ? N : kAhead;
+    __builtin_amdgcn_sched_group_barrier(0x100, A, 0);              // DS read
+#pragma unroll
+    for (int i = 0; i < N - A; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);          // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, A, 0);              // MFMA
+}
+
 // head_dim 256 needs the whole register file for one wave per SIMD: one
 // group of 4 waves that runs each tile's QK, softmax and P.V in turn.
 template <int D> struct Groups { static constexpr int N = D >= 256 ? 1 : 2; };
@@ -313,41 +390,110 @@ void prefill_attn(AttnParams P) {
     const int tic = valid ? ti : P.n - 1;
     const int h = g * G + col % G;
     const int qpos = P.pos0 + tic;
+    // Every load of q and of its sin/cos rows is issued before any
+    // arithmetic: the empty asm statements take all of them at once and hand
+    // back opaque values, which the compiler can neither sink below the math
+    // nor reload later, so the prologue costs one memory round trip instead
+    // of one per batch of loads.
+    auto hold = [](float4& v) __attribute__((always_inline)) {
+        __asm__ volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+    };
+    auto unpack = [](const float4& a, const float4& b, float (&x)[8]) __attribute__((always_inline)) {
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    };
+    auto to_qt = [&](const float (&y)[8]) __attribute__((always_inline)) {
+        h8 v;
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (_Float16)(y[e] * P.qscale);
+        return v;
+    };
+    const float* qrow = P.q + ((size_t)tic * P.H + h) * D;
+    const float* srow = P.rope_sin + (size_t)qpos * P.half;
+    const float* crow = P.rope_cos + (size_t)qpos * P.half;
+    constexpr int KH = HALF % 16 == 0 ? HALF / 16 : 1;    // k-steps holding rotated first halves
+    // With two groups, each loads and rotates half of the rotation pairs
+    // (k-steps kh and kh + KH for its kh) and hands its fp16 k-steps to the
+    // other through LDS: K slot 3 (group 0's) and V slot 1 (group 1's), whose
+    // first direct loads come in phase 1, after the phase-0 barrier.
+    constexpr bool kSplitQ = NG == 2 && KH >= 2 && 2 * KH == NKS;
     h8 qt[NKS];
-    {
-        const float* qrow = P.q + ((size_t)tic * P.H + h) * D;
-        float x[NKS][8];
+    if constexpr (kSplitQ) {
+        constexpr int KO = KH / 2;
+        static_assert(2 * KO * 4 * 64 * 16 <= TL::K_ELEMS * 2 && 2 * KO * 4 * 64 * 16 <= TL::V_ELEMS * 2,
+                      "q exchange fits a ring slot");
+        const int kh0 = grp * KO;
+        float4 xa[2 * KO], xb[2 * KO], sa[KO], sb[KO], ca[KO], cb[KO];
+#pragma unroll
+        for (int i = 0; i < KO; i++) {
+            const int ks = kh0 + i;
+            xa[i] = *reinterpret_cast<const float4*>(qrow + 16 * ks + 8 * hh);
+            xb[i] = *reinterpret_cast<const float4*>(qrow + 16 * ks + 8 * hh + 4);
+            xa[KO + i] = *reinterpret_cast<const float4*>(qrow + 16 * (ks + KH) + 8 * hh);
+            xb[KO + i] = *reinterpret_cast<const float4*>(qrow + 16 * (ks + KH) + 8 * hh + 4);
+            sa[i] = *reinterpret_cast<const float4*>(srow + 16 * ks + 8 * hh);
+            sb[i] = *reinterpret_cast<const float4*>(srow + 16 * ks + 8 * hh + 4);
+            ca[i] = *reinterpret_cast<const float4*>(crow + 16 * ks + 8 * hh);
+            cb[i] = *reinterpret_cast<const float4*>(crow + 16 * ks + 8 * hh + 4);
+        }
+#pragma unroll
+        for (int i = 0; i < 2 * KO; i++) { hold(xa[i]); hold(xb[i]); }
+#pragma unroll
+        for (int i = 0; i < KO; i++) { hold(sa[i]); hold(sb[i]); hold(ca[i]); hold(cb[i]); }
+        h8* xq = reinterpret_cast<h8*>(grp == 0 ? k3 : v1);
+#pragma unroll
+        for (int i = 0; i < KO; i++) {
+            float x0[8], x1[8], sn[8], cs[8], y0[8], y1[8];
+            unpack(xa[i], xb[i], x0);
+            unpack(xa[KO + i], xb[KO + i], x1);
+            unpack(sa[i], sb[i], sn);
+            unpack(ca[i], cb[i], cs);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                y0[e] = fmaf(cs[e], x0[e], -(sn[e] * x1[e]));
+                y1[e] = fmaf(sn[e], x0[e], cs[e] * x1[e]);
+            }
+            xq[(i * 4 + sub) * 64 + lane] = to_qt(y0);
+            xq[((KO + i) * 4 + sub) * 64 + lane] = to_qt(y1);
+        }
+    } else {
+        float4 xa[NKS], xb[NKS], sa[KH], sb[KH], ca[KH], cb[KH];
+        const int rofs = HALF % 16 == 0 ? 8 * hh : 0;   // D = 16: both halves read [0, 8)
 #pragma unroll
         for (int ks = 0; ks < NKS; ks++) {
-            const float4 a = *reinterpret_cast<const float4*>(qrow + 16 * ks + 8 * hh);
-            const float4 b = *reinterpret_cast<const float4*>(qrow + 16 * ks + 8 * hh + 4);
-            x[ks][0] = a.x; x[ks][1] = a.y; x[ks][2] = a.z; x[ks][3] = a.w;
-            x[ks][4] = b.x; x[ks][5] = b.y; x[ks][6] = b.z; x[ks][7] = b.w;
+            xa[ks] = *reinterpret_cast<const float4*>(qrow + 16 * ks + 8 * hh);
+            xb[ks] = *reinterpret_cast<const float4*>(qrow + 16 * ks + 8 * hh + 4);
         }
-        const float* srow = P.rope_sin + (size_t)qpos * P.half;
-        const float* crow = P.rope_cos + (size_t)qpos * P.half;
+#pragma unroll
+        for (int ks = 0; ks < KH; ks++) {
+            sa[ks] = *reinterpret_cast<const float4*>(srow + 16 * ks + rofs);
+            sb[ks] = *reinterpret_cast<const float4*>(srow + 16 * ks + rofs + 4);
+            ca[ks] = *reinterpret_cast<const float4*>(crow + 16 * ks + rofs);
+            cb[ks] = *reinterpret_cast<const float4*>(crow + 16 * ks + rofs + 4);
+        }
+#pragma unroll
+        for (int ks = 0; ks < NKS; ks++) { hold(xa[ks]); hold(xb[ks]); }
+#pragma unroll
+        for (int ks = 0; ks < KH; ks++) { hold(sa[ks]); hold(sb[ks]); hold(ca[ks]); hold(cb[ks]); }
+        float x[NKS][8], sn[KH][8], cs[KH][8];
+#pragma unroll
+        for (int ks = 0; ks < NKS; ks++) unpack(xa[ks], xb[ks], x[ks]);
+#pragma unroll
+        for (int ks = 0; ks < KH; ks++) {
+            unpack(sa[ks], sb[ks], sn[ks]);
+            unpack(ca[ks], cb[ks], cs[ks]);
+        }
         float y[NKS][8];
         if constexpr (HALF % 16 == 0) {
             // d and d + HALF sit in the same lane, k-steps ks and ks + HALF/16.
-            constexpr int KH = HALF / 16;
 #pragma unroll
-            for (int ks = 0; ks < KH; ks++) {
-                float sn[8], cs[8];
-                const float4 s0 = *reinterpret_cast<const float4*>(srow + 16 * ks + 8 * hh);
-                const float4 s1 = *reinterpret_cast<const float4*>(srow + 16 * ks + 8 * hh + 4);
-                const float4 c0 = *reinterpret_cast<const float4*>(crow + 16 * ks + 8 * hh);
-                const float4 c1 = *reinterpret_cast<const float4*>(crow + 16 * ks + 8 * hh + 4);
-                sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w;
-                sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
-                cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w;
-                cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
+            for (int ks = 0; ks < KH; ks++)
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const float a = x[ks][e], b = x[ks + KH][e];
-                    y[ks][e] = fmaf(cs[e], a, -(sn[e] * b));
-                    y[ks + KH][e] = fmaf(sn[e], a, cs[e] * b);
+                    y[ks][e] = fmaf(cs[ks][e], a, -(sn[ks][e] * b));
+                    y[ks + KH][e] = fmaf(sn[ks][e], a, cs[ks][e] * b);
                 }
-            }
 #pragma unroll
             for (int ks = 2 * KH; ks < NKS; ks++)
 #pragma unroll
@@ -355,27 +501,16 @@ void prefill_attn(AttnParams P) {
         } else {
             // D = 16: HALF = 8, the partner of d is in lane l ^ 32.
             static_assert(NKS == 1 && HALF == 8, "only D = 16 pairs across lanes");
-            const float4 s0 = *reinterpret_cast<const float4*>(srow);
-            const float4 s1 = *reinterpret_cast<const float4*>(srow + 4);
-            const float4 c0 = *reinterpret_cast<const float4*>(crow);
-            const float4 c1 = *reinterpret_cast<const float4*>(crow + 4);
-            const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-            const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const float other = __shfl_xor(x[0][e], 32);
                 const float a = hh ? other : x[0][e];    // element d
                 const float b = hh ? x[0][e] : other;    // element d + 8
-                y[0][e] = hh ? fmaf(sn[e], a, cs[e] * b) : fmaf(cs[e], a, -(sn[e] * b));
+                y[0][e] = hh ? fmaf(sn[0][e], a, cs[0][e] * b) : fmaf(cs[0][e], a, -(sn[0][e] * b));
             }
         }
 #pragma unroll
-        for (int ks = 0; ks < NKS; ks++) {
-            h8 v;
-#pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = (_Float16)(y[ks][e] * P.qscale);
-            qt[ks] = v;
-        }
+        for (int ks = 0; ks < NKS; ks++) qt[ks] = to_qt(y[ks]);
     }
 
     f32x16 acc[NDB];
@@ -388,36 +523,52 @@ void prefill_attn(AttnParams P) {
     h8 pt[NT];                     // its fp16 weights, B operands of P^T
 
     // S^T block kb: rows = keys kb*32 + 8(r/4) + 4hh + r%4 of the tile,
-    // column = l32.
+    // column = l32.  The K fragments of block kb + 1 are read while block
+    // kb's MFMAs run, so no MFMA waits on its own LDS read.
     auto qk = [&](const _Float16* sk) __attribute__((always_inline)) {
-#pragma unroll
-        for (int kb = 0; kb < NKB; kb++) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) S[kb][r] = 0.0f;
+        h8 a[2][NKS];
+        auto fetch = [&](int kb, h8 (&dst)[NKS]) __attribute__((always_inline)) {
             const _Float16* krow = sk + (kb * 32 + l32) * TL::KS + 8 * hh;
 #pragma unroll
-            for (int ks = 0; ks < NKS; ks++) {
-                const h8 a = *reinterpret_cast<const h8*>(krow + 16 * ks);
-                S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qt[ks], S[kb], 0, 0, 0);
-            }
+            for (int ks = 0; ks < NKS; ks++) dst[ks] = *reinterpret_cast<const h8*>(krow + 16 * ks);
+        };
+        fetch(0, a[0]);
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
+            if (kb + 1 < NKB) fetch(kb + 1, a[(kb + 1) & 1]);
+#pragma unroll
+            for (int r = 0; r < 16; r++) S[kb][r] = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < NKS; ks++)
+                S[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[kb & 1][ks], qt[ks], S[kb], 0, 0, 0);
         }
+        pipeline_order<NKB * NKS>();
     };
     // O^T block b += V^T[32b + l32][keys of step t] * P^T[t].  The k index
     // 8hh + c of step t = (kb, tt) is key kb*32 + 16tt + 4hh + c for c < 4 and
     // kb*32 + 16tt + 8 + 4hh + (c - 4) for c >= 4: the order in which the S^T
-    // accumulator holds them.
+    // accumulator holds them.  Block b + 1's V^T fragments are read while
+    // block b's MFMAs run.
     auto pv = [&](const _Float16* sv) __attribute__((always_inline)) {
-#pragma unroll
-        for (int b = 0; b < NDB; b++) {
+        h8 a[2][NT];
+        auto fetch = [&](int b, h8 (&dst)[NT]) __attribute__((always_inline)) {
             const _Float16* vrow = sv + (32 * b + l32) * TL::VS + 4 * hh;
 #pragma unroll
             for (int t = 0; t < NT; t++) {
                 const h4 lo = *reinterpret_cast<const h4*>(vrow + 16 * t);
                 const h4 hi = *reinterpret_cast<const h4*>(vrow + 16 * t + 8);
-                const h8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pt[t], acc[b], 0, 0, 0);
+                dst[t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
             }
+        };
+        fetch(0, a[0]);
+#pragma unroll
+        for (int b = 0; b < NDB; b++) {
+            if (b + 1 < NDB) fetch(b + 1, a[(b + 1) & 1]);
+#pragma unroll
+            for (int t = 0; t < NT; t++)
+                acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[b & 1][t], pt[t], acc[b], 0, 0, 0);
         }
+        pipeline_order<NDB * NT>();
     };
     // Online softmax of tile t's scores: causal mask near the diagonal, lazy
     // running max (the accumulator is rescaled only when the max grows by
@@ -432,11 +583,13 @@ void prefill_attn(AttnParams P) {
                     if (key > qpos) S[kb][r] = -INFINITY;
                 }
         }
-        float mt = -INFINITY;
+        // Tile max as a tree of four partial maxima (short dependency chain).
+        float mp[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) mt = fmaxf(mt, S[kb][r]);
+            for (int r = 0; r < 16; r++) mp[r & 3] = fmaxf(mp[r & 3], S[kb][r]);
+        float mt = fmaxf(fmaxf(mp[0], mp[1]), fmaxf(mp[2], mp[3]));
         mt = max_halves(mt);
         const bool need = mt > m_run + kTau;
         if (__builtin_amdgcn_ballot_w64(need)) {
@@ -455,6 +608,7 @@ void prefill_attn(AttnParams P) {
         const float msub = m_run == -INFINITY ? 0.0f : m_run;
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
         const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+        float lp[4] = {0.0f, 0.0f, 0.0f, 0.0f};   // four independent row-sum chains
 #pragma unroll
         for (int t2 = 0; t2 < NT; t2++) {
             h8 v;
@@ -465,13 +619,25 @@ void prefill_attn(AttnParams P) {
 #pragma unroll
             for (int c = 0; c < 8; c += 2) {
                 const h2 p2 = {v[c], v[c + 1]};
-                l_run = __builtin_amdgcn_fdot2(p2, one, l_run, false);
+                lp[c >> 1] = __builtin_amdgcn_fdot2(p2, one, lp[c >> 1], false);
             }
         }
+        l_run += (lp[0] + lp[1]) + (lp[2] + lp[3]);
     };
 
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if constexpr (kSplitQ) {
+        // k-step ks = kh (+ KH) was written by group kh / (KH / 2) at index
+        // (kh % (KH / 2)) (+ KH / 2).
+        constexpr int KO = KH / 2;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ks++) {
+            const int kh = ks % KH, i = kh % KO + (ks >= KH ? KO : 0);
+            const h8* xq = reinterpret_cast<const h8*>(kh / KO == 0 ? k3 : v1);
+            qt[ks] = xq[(i * 4 + sub) * 64 + lane];
+        }
+    }
 
     // Phase p (p = 0 .. ntile + 1): the group p % 2 runs MFMAs -- P.V of
     // tile p - 2 (its previous tile) and QK of tile p -- while the other
@@ -493,8 +659,17 @@ void prefill_attn(AttnParams P) {
             }
         }
     };
-    auto sync = [&]() __attribute__((always_inline)) {
-        __builtin_amdgcn_s_waitcnt(0);
+    // End of phase p: wait for this wave's loads from phase p - 1 (the ones
+    // phase p + 1 reads), leaving phase p's own loads in flight, then the
+    // barrier makes every wave's completed loads visible.
+    const int nk = copy_count<TL::K_ELEMS * 2, kAttnWaves>(w);
+    const int nv = copy_count<TL::V_ELEMS * 2, kAttnWaves>(w);
+    auto issued = [&](int p) __attribute__((always_inline)) {
+        if constexpr (NG == 2) return (p + 2 < ntile ? nk : 0) + (p < ntile ? nv : 0);
+        else return p + 2 < ntile ? nk + nv : 0;
+    };
+    auto sync_p = [&](int p) __attribute__((always_inline)) {
+        wait_vmcnt(issued(p));
         __syncthreads();
     };
     auto mphase = [&](int p, int R) __attribute__((always_inline)) {
@@ -508,23 +683,23 @@ void prefill_attn(AttnParams P) {
     if constexpr (NG == 2) {
         if (grp == 0) {
             for (int p = 0; p < nphase; p += 4) {
-                dma(p, 0); mphase(p, 0); sync();
+                dma(p, 0); mphase(p, 0); sync_p(p);
                 if (p + 1 >= nphase) break;
-                dma(p + 1, 1); vphase(p + 1); sync();
+                dma(p + 1, 1); vphase(p + 1); sync_p(p + 1);
                 if (p + 2 >= nphase) break;
-                dma(p + 2, 2); mphase(p + 2, 2); sync();
+                dma(p + 2, 2); mphase(p + 2, 2); sync_p(p + 2);
                 if (p + 3 >= nphase) break;
-                dma(p + 3, 3); vphase(p + 3); sync();
+                dma(p + 3, 3); vphase(p + 3); sync_p(p + 3);
             }
         } else {
             for (int p = 0; p < nphase; p += 4) {
-                dma(p, 0); vphase(p); sync();
+                dma(p, 0); vphase(p); sync_p(p);
                 if (p + 1 >= nphase) break;
-                dma(p + 1, 1); mphase(p + 1, 1); sync();
+                dma(p + 1, 1); mphase(p + 1, 1); sync_p(p + 1);
                 if (p + 2 >= nphase) break;
-                dma(p + 2, 2); vphase(p + 2); sync();
+                dma(p + 2, 2); vphase(p + 2); sync_p(p + 2);
                 if (p + 3 >= nphase) break;
-                dma(p + 3, 3); mphase(p + 3, 3); sync();
+                dma(p + 3, 3); mphase(p + 3, 3); sync_p(p + 3);
             }
         }
     } else {
@@ -536,7 +711,7 @@ void prefill_attn(AttnParams P) {
                 softmax(p);
                 pv(vslot[R]);
             }
-            sync();
+            sync_p(p);
         };
         for (int p = 0; p < nphase; p += 4) {
             whole(p, 0);
@@ -547,19 +722,40 @@ void prefill_attn(AttnParams P) {
     }
 
     // ---- merge the groups' (m, l, o) and write O[d][column] for
-    // d = 32b + 8(r/4) + 4hh + r%4.  Group 1 hands its state to group 0
-    // through a dedicated LDS buffer, one 32-row block of O^T at a time.
-    __shared__ float xm[NG == 2 ? 4 * 2 * 64 : 1];
-    __shared__ float xo[NG == 2 ? 4 * 16 * 64 : 1];
+    // d = 32b + 8(r/4) + 4hh + r%4.  One exchange: block b of O^T is
+    // finished by group owner(b) (the first half of the blocks by group 0,
+    // the rest by group 1), and the other group hands its partial block b
+    // over through LDS -- the K ring slots, free once the last phase's
+    // barrier has passed, when they are large enough, else a dedicated
+    // buffer.  Lane (l32, hh) of wave `sub` holds the same (d, column) in
+    // both groups, so each lane reads back exactly what its partner wrote.
+    constexpr int XBLK = 4 * 16 * 64;                      // floats per exchanged block
+    constexpr bool kInRing = TL::K_ELEMS * 2 >= XBLK * 4 && NDB <= kSlots;
+    __shared__ __attribute__((aligned(16))) float xm[NG == 2 ? 2 * 4 * 2 * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float xo[NG == 2 && !kInRing ? NDB * XBLK : 1];
+    auto owner = [&](int b) __attribute__((always_inline)) { return NDB == 1 ? 0 : (b < NDB / 2 ? 0 : 1); };
+    auto xbuf = [&](int b) __attribute__((always_inline)) -> float* {
+        if constexpr (kInRing) return reinterpret_cast<float*>(kslot[b]);
+        else return xo + b * XBLK;
+    };
     float fa = 1.0f, fb = 0.0f, inv;
     if constexpr (NG == 2) {
-        if (grp == 1) {
-            xm[(sub * 2 + 0) * 64 + lane] = m_run;
-            xm[(sub * 2 + 1) * 64 + lane] = l_run;
+        xm[((grp * 4 + sub) * 2 + 0) * 64 + lane] = m_run;
+        xm[((grp * 4 + sub) * 2 + 1) * 64 + lane] = l_run;
+#pragma unroll
+        for (int b = 0; b < NDB; b++) {
+            if (owner(b) != grp) {
+                float4* dst = reinterpret_cast<float4*>(xbuf(b));
+#pragma unroll
+                for (int r4 = 0; r4 < 4; r4++)
+                    dst[(sub * 4 + r4) * 64 + lane] = make_float4(acc[b][4 * r4], acc[b][4 * r4 + 1], acc[b][4 * r4 + 2],
+                                               acc[b][4 * r4 + 3]);
+            }
         }
         __syncthreads();
-        const float mb = xm[(sub * 2 + 0) * 64 + lane];
-        const float lb = xm[(sub * 2 + 1) * 64 + lane];
+        const int og = grp ^ 1;
+        const float mb = xm[((og * 4 + sub) * 2 + 0) * 64 + lane];
+        const float lb = xm[((og * 4 + sub) * 2 + 1) * 64 + lane];
         const float M = fmaxf(m_run, mb);
         fa = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
         fb = mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb - M);
@@ -567,31 +763,23 @@ void prefill_attn(AttnParams P) {
     } else {
         inv = 1.0f / sum_halves(l_run);
     }
+    if (!valid) return;
     float* orow = P.out + ((size_t)ti * P.H + h) * D;
 #pragma unroll
     for (int b = 0; b < NDB; b++) {
-        if constexpr (NG == 2) {
-            if (grp == 1) {
+        if (NG == 2 && owner(b) != grp) continue;
 #pragma unroll
-                for (int r = 0; r < 16; r++) xo[(sub * 16 + r) * 64 + lane] = acc[b][r];
-            }
-            __syncthreads();
+        for (int r4 = 0; r4 < 4; r4++) {
+            const int d = 32 * b + 8 * r4 + 4 * hh;
+            float4 ob = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if constexpr (NG == 2) ob = reinterpret_cast<const float4*>(xbuf(b))[(sub * 4 + r4) * 64 + lane];
+            float4 o;
+            o.x = (acc[b][4 * r4 + 0] * fa + ob.x * fb) * inv;
+            o.y = (acc[b][4 * r4 + 1] * fa + ob.y * fb) * inv;
+            o.z = (acc[b][4 * r4 + 2] * fa + ob.z * fb) * inv;
+            o.w = (acc[b][4 * r4 + 3] * fa + ob.w * fb) * inv;
+            if (d < D) *reinterpret_cast<float4*>(orow + d) = o;
         }
-        if (grp == 0 && valid) {
-#pragma unroll
-            for (int r4 = 0; r4 < 4; r4++) {
-                const int d = 32 * b + 8 * r4 + 4 * hh;
-                float o[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int r = 4 * r4 + e;
-                    const float ob = NG == 2 ? xo[(sub * 16 + r) * 64 + lane] : 0.0f;
-                    o[e] = (acc[b][r] * fa + ob * fb) * inv;
-                }
-                if (d < D) *reinterpret_cast<float4*>(orow + d) = make_float4(o[0], o[1], o[2], o[3]);
-            }
-        }
-        if constexpr (NG == 2) __syncthreads();
     }
 }
 
@@ -622,7 +810,7 @@ int launch_dg(const PrefillArgs& a, hipStream_t st) {
     S.HK = HK;
     S.T = T;
     S.tiles = static_cast<_Float16*>(tiles);
-    hipLaunchKernelGGL((prefill_stage<D, CT>), dim3(T, HK), dim3(kThreads), 0, st, S);
+    hipLaunchKernelGGL((prefill_stage<D, CT>), dim3(T * (TL::KT / StageRows<D>::N), HK), dim3(kThreads), 0, st, S);
     PKH_HIP(hipGetLastError());
 
     constexpr int BM = kCols / G;
