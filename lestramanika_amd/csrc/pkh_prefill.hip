@@ -52,6 +52,7 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKPad = 8;        // fp16 padding per K row (conflict-free ds_read_b128)
 constexpr int kVPad = 4;        // fp16 padding per V^T row (conflict-free ds_read_b64)
@@ -84,8 +85,9 @@ __device__ __forceinline__ void load4(const _Float16* p, float (&x)[4]) {
     const h4 v = *reinterpret_cast<const h4*>(p);
     for (int i = 0; i < 4; i++) x[i] = (float)v[i];
 }
+// Cache rows are stored non-temporally: this launch never reads them back.
 __device__ __forceinline__ void store4(float* p, const float (&x)[4]) {
-    *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    __builtin_nontemporal_store(f32x4{x[0], x[1], x[2], x[3]}, reinterpret_cast<f32x4*>(p));
 }
 // fp32 -> fp16, round to nearest even, of a value already rounded to fp32.
 // The empty asm keeps the compiler from folding the conversion into the
@@ -101,7 +103,7 @@ __device__ __forceinline__ h4 to_h4(const float (&x)[4]) {
     return v;
 }
 __device__ __forceinline__ void store4(_Float16* p, const float (&x)[4]) {
-    *reinterpret_cast<h4*>(p) = to_h4(x);
+    __builtin_nontemporal_store(to_h4(x), reinterpret_cast<h4*>(p));
 }
 
 // ---- stage: append + fp16 tiles -------------------------------------------
@@ -763,21 +765,60 @@ void prefill_attn(AttnParams P) {
     } else {
         inv = 1.0f / sum_halves(l_run);
     }
+    if constexpr (NG == 2) {
+        // Owned block b: read the partner's partial (4 KB of xbuf(b) per
+        // wave), then restage the finished block in that same region as
+        // [column][16-byte unit] with the unit index XORed by column % 8
+        // (conflict-free both ways), and write it back row-contiguous: each
+        // store instruction covers 8 columns x 128 bytes, whole cache lines
+        // of O instead of 32-byte pieces of 32 rows.  The stores are
+        // non-temporal: O is not read again here, and streaming it out as it
+        // is produced keeps 32 MB of dirty lines (a 2048-token layer) from
+        // being written back all at once when the kernel ends.
+#pragma unroll
+        for (int b = 0; b < NDB; b++) {
+            if (owner(b) != grp) continue;
+            float4* st = reinterpret_cast<float4*>(xbuf(b)) + sub * 256;
+            float4 ob[4];
+#pragma unroll
+            for (int r4 = 0; r4 < 4; r4++) ob[r4] = st[r4 * 64 + lane];
+#pragma unroll
+            for (int r4 = 0; r4 < 4; r4++) {
+                float4 o;
+                o.x = (acc[b][4 * r4 + 0] * fa + ob[r4].x * fb) * inv;
+                o.y = (acc[b][4 * r4 + 1] * fa + ob[r4].y * fb) * inv;
+                o.z = (acc[b][4 * r4 + 2] * fa + ob[r4].z * fb) * inv;
+                o.w = (acc[b][4 * r4 + 3] * fa + ob[r4].w * fb) * inv;
+                const int u = 2 * r4 + hh;
+                st[l32 * 8 + (u ^ (l32 & 7))] = o;
+            }
+            const int u = lane & 7;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int c = 8 * i + (lane >> 3);
+                const float4 o = st[c * 8 + (u ^ (c & 7))];
+                const int cg = 32 * sub + c;
+                const int tc = qb * BM + cg / G;
+                const int d = 32 * b + 4 * u;
+                if (tc < P.n && d < D)
+                    __builtin_nontemporal_store(__builtin_bit_cast(f32x4, o),
+                                                reinterpret_cast<f32x4*>(P.out + ((size_t)tc * P.H + g * G + cg % G) * D + d));
+            }
+        }
+        return;
+    }
     if (!valid) return;
     float* orow = P.out + ((size_t)ti * P.H + h) * D;
 #pragma unroll
     for (int b = 0; b < NDB; b++) {
-        if (NG == 2 && owner(b) != grp) continue;
 #pragma unroll
         for (int r4 = 0; r4 < 4; r4++) {
             const int d = 32 * b + 8 * r4 + 4 * hh;
-            float4 ob = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if constexpr (NG == 2) ob = reinterpret_cast<const float4*>(xbuf(b))[(sub * 4 + r4) * 64 + lane];
             float4 o;
-            o.x = (acc[b][4 * r4 + 0] * fa + ob.x * fb) * inv;
-            o.y = (acc[b][4 * r4 + 1] * fa + ob.y * fb) * inv;
-            o.z = (acc[b][4 * r4 + 2] * fa + ob.z * fb) * inv;
-            o.w = (acc[b][4 * r4 + 3] * fa + ob.w * fb) * inv;
+            o.x = acc[b][4 * r4 + 0] * inv;
+            o.y = acc[b][4 * r4 + 1] * inv;
+            o.z = acc[b][4 * r4 + 2] * inv;
+            o.w = acc[b][4 * r4 + 3] * inv;
             if (d < D) *reinterpret_cast<float4*>(orow + d) = o;
         }
     }
