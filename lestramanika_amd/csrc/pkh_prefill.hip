@@ -37,7 +37,7 @@
 //                key tiles by parity and alternate phases, so that while one
 //                group's waves issue MFMAs the other's run the softmax; the
 //                groups' (m, l, o) are merged at the end.  Tiles reach LDS
-//                through gfx950 direct loads (global_load_lds_dwordx4) into
+//                through gfx950 direct loads (buffer_load_dwordx4 ... lds) into
 //                4-slot K and V rings, two phases ahead of use.
 
 #include "pkh_internal.h"
@@ -267,22 +267,27 @@ __device__ __forceinline__ float sum_halves(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Copy `bytes` (a multiple of 16) from global memory to LDS with the gfx950
-// direct loads: each instruction moves 1 KB, lane l's 16 bytes landing at
-// dst + 16*l.  Instructions are dealt round-robin to the waves; the data is
-// visible to the workgroup after s_waitcnt vmcnt(0) and a barrier.
+// Copy BYTES (a multiple of 16) from a buffer to LDS with gfx950 direct
+// loads (buffer_load_dwordx4 ... lds): each instruction moves 1 KB, lane l's
+// 16 bytes landing at dst + 16*l.  The tile offset goes in the scalar
+// offset, the lane's 16-byte chunk in the vector offset.  Instructions are
+// dealt round-robin to the waves; the data is visible to the workgroup after
+// the issuing waves' s_waitcnt vmcnt and a barrier.  (The MUBUF form, unlike
+// global_load_lds, lets the compiler keep counting LDS reads precisely while
+// these loads are in flight: it waits lgkmcnt(n) for the one fragment an
+// MFMA needs instead of lgkmcnt(0) for all of them.)
 template <int BYTES, int WAVES>
-__device__ __forceinline__ void copy_to_lds(_Float16* dst, const _Float16* src, int wave, int lane) {
+__device__ __forceinline__ void copy_to_lds(_Float16* dst, __amdgpu_buffer_rsrc_t rs, unsigned src_bytes, int wave,
+                                            int lane) {
     constexpr int CH = BYTES / 16;                 // 16-byte chunks
     constexpr int NI = (CH + 63) / 64;             // wave instructions
 #pragma unroll
     for (int i = wave; i < NI; i += WAVES) {
         const int c = 64 * i + lane;
         if (NI * 64 == CH || c < CH)
-            __builtin_amdgcn_global_load_lds(
-                reinterpret_cast<const void*>(reinterpret_cast<const char*>(src) + 16 * c),
-                (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(dst) + 1024 * i),
-                16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(dst) + 1024 * i), 16,
+                16u * (unsigned)c, src_bytes, 0, 0);
     }
 }
 
@@ -304,6 +309,14 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
         default: __builtin_amdgcn_s_waitcnt(0xF70); break;
     }
 }
+
+// Workgroup barrier with no memory fence.  __syncthreads() is a
+// workgroup-scope release, and the compiler completes every direct load
+// (they write LDS) before it -- including the ones just issued for two phases
+// later.  The phase loop instead waits per wave, with wait_vmcnt, for exactly
+// the loads the next phase reads; LDS reads are consumed (and so complete)
+// within their phase, long before a later direct load reuses their slot.
+__device__ __forceinline__ void phase_barrier() { __asm__ volatile("s_barrier" ::: "memory"); }
 
 // Direct-load instructions a wave issues for one copy_to_lds<BYTES, WAVES>.
 template <int BYTES, int WAVES>
@@ -369,12 +382,14 @@ void prefill_attn(AttnParams P) {
     const int qmax = P.pos0 + min(qb * BM + BM - 1, P.n - 1);
     const int ntile = qmax / KT + 1;
 
-    const _Float16* src = P.tiles + (size_t)g * P.T * TL::ELEMS;
+    // This KV head's tiles as one buffer (reads past its end return zero).
+    const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(P.tiles + (size_t)g * P.T * TL::ELEMS), (short)0, P.T * TL::BYTES, 0x00020000);
     auto load_k = [&](_Float16* dst, int t) __attribute__((always_inline)) {
-        copy_to_lds<TL::K_ELEMS * 2, kAttnWaves>(dst, src + (size_t)t * TL::ELEMS, w, lane);
+        copy_to_lds<TL::K_ELEMS * 2, kAttnWaves>(dst, trs, (unsigned)(t * TL::BYTES), w, lane);
     };
     auto load_v = [&](_Float16* dst, int t) __attribute__((always_inline)) {
-        copy_to_lds<TL::V_ELEMS * 2, kAttnWaves>(dst, src + (size_t)t * TL::ELEMS + TL::K_ELEMS, w, lane);
+        copy_to_lds<TL::V_ELEMS * 2, kAttnWaves>(dst, trs, (unsigned)(t * TL::BYTES + TL::K_ELEMS * 2), w, lane);
     };
     load_k(k0, 0);
     if (ntile > 1) load_k(k1, 1);
@@ -672,7 +687,7 @@ void prefill_attn(AttnParams P) {
     };
     auto sync_p = [&](int p) __attribute__((always_inline)) {
         wait_vmcnt(issued(p));
-        __syncthreads();
+        phase_barrier();
     };
     auto mphase = [&](int p, int R) __attribute__((always_inline)) {
         if (p >= 2 && p - 2 < ntile) pv(vslot[(R + 2) % kSlots]);
