@@ -296,34 +296,13 @@ __device__ __forceinline__ void copy_to_lds(_Float16* dst, __amdgpu_buffer_rsrc_
 // group 0 takes the even key tiles and group 1 the odd ones (split-K), and
 // the groups alternate phases: while one group's waves run MFMAs the other
 // group's run the softmax on the VALU.
-// s_waitcnt vmcnt(n) for a wave-uniform n < 16 (lgkmcnt and expcnt are not
-// waited on): returns once at most n of this wave's vector-memory operations
-// are outstanding.  Loads complete in order, so this waits for everything
-// issued before the last n.
-__device__ __forceinline__ void wait_vmcnt(int n) {
-    switch (n) {
-#define PKH_VM(N) case N: __builtin_amdgcn_s_waitcnt(0xF70 | N); break;
-        PKH_VM(0) PKH_VM(1) PKH_VM(2) PKH_VM(3) PKH_VM(4) PKH_VM(5) PKH_VM(6) PKH_VM(7)
-        PKH_VM(8) PKH_VM(9) PKH_VM(10) PKH_VM(11) PKH_VM(12) PKH_VM(13) PKH_VM(14)
-#undef PKH_VM
-        default: __builtin_amdgcn_s_waitcnt(0xF70); break;
-    }
-}
-
 // Workgroup barrier with no memory fence.  __syncthreads() is a
 // workgroup-scope release, and the compiler completes every direct load
-// (they write LDS) before it -- including the ones just issued for two phases
-// later.  The phase loop instead waits per wave, with wait_vmcnt, for exactly
-// the loads the next phase reads; LDS reads are consumed (and so complete)
-// within their phase, long before a later direct load reuses their slot.
+// (they write LDS) before it -- including loads just issued for a later
+// phase.  The phase loop waits for its own loads explicitly before this
+// barrier; LDS reads are consumed (and so complete) within their phase, long
+// before a later direct load reuses their slot.
 __device__ __forceinline__ void phase_barrier() { __asm__ volatile("s_barrier" ::: "memory"); }
-
-// Direct-load instructions a wave issues for one copy_to_lds<BYTES, WAVES>.
-template <int BYTES, int WAVES>
-__device__ __forceinline__ int copy_count(int wave) {
-    constexpr int NI = (BYTES / 16 + 63) / 64;
-    return (NI - wave + WAVES - 1) / WAVES;
-}
 
 // Issue order for a run of N MFMAs that each consume one LDS fragment: the
 // first kAhead fragment reads, then one MFMA and the next read in turn, so
@@ -391,11 +370,16 @@ void prefill_attn(AttnParams P) {
     auto load_v = [&](_Float16* dst, int t) __attribute__((always_inline)) {
         copy_to_lds<TL::V_ELEMS * 2, kAttnWaves>(dst, trs, (unsigned)(t * TL::BYTES + TL::K_ELEMS * 2), w, lane);
     };
+    // Tiles for the first phases (the loop's phase p issues the loads of
+    // phase p + 1 at its end): K(0), K(1), K(2) and V(0) with two groups;
+    // K and V of tiles 0, 1, 2 with one.
     load_k(k0, 0);
     if (ntile > 1) load_k(k1, 1);
+    if (ntile > 2) load_k(k2, 2);
+    load_v(v0, 0);
     if constexpr (NG == 1) {
-        load_v(v0, 0);
         if (ntile > 1) load_v(v1, 1);
+        if (ntile > 2) load_v(v2, 2);
     }
 
     // ---- q: load, rotate (same contraction as the reference), scale, fp16.
@@ -431,8 +415,9 @@ void prefill_attn(AttnParams P) {
     constexpr int KH = HALF % 16 == 0 ? HALF / 16 : 1;    // k-steps holding rotated first halves
     // With two groups, each loads and rotates half of the rotation pairs
     // (k-steps kh and kh + KH for its kh) and hands its fp16 k-steps to the
-    // other through LDS: K slot 3 (group 0's) and V slot 1 (group 1's), whose
-    // first direct loads come in phase 1, after the phase-0 barrier.
+    // other through LDS: V slots 2 (group 0's) and 3 (group 1's), whose first
+    // direct loads are issued at the end of phases 1 and 2, after the phase-0
+    // barrier.
     constexpr bool kSplitQ = NG == 2 && KH >= 2 && 2 * KH == NKS;
     h8 qt[NKS];
     if constexpr (kSplitQ) {
@@ -457,7 +442,7 @@ void prefill_attn(AttnParams P) {
         for (int i = 0; i < 2 * KO; i++) { hold(xa[i]); hold(xb[i]); }
 #pragma unroll
         for (int i = 0; i < KO; i++) { hold(sa[i]); hold(sb[i]); hold(ca[i]); hold(cb[i]); }
-        h8* xq = reinterpret_cast<h8*>(grp == 0 ? k3 : v1);
+        h8* xq = reinterpret_cast<h8*>(grp == 0 ? v2 : v3);
 #pragma unroll
         for (int i = 0; i < KO; i++) {
             float x0[8], x1[8], sn[8], cs[8], y0[8], y1[8];
@@ -651,7 +636,7 @@ void prefill_attn(AttnParams P) {
 #pragma unroll
         for (int ks = 0; ks < NKS; ks++) {
             const int kh = ks % KH, i = kh % KO + (ks >= KH ? KO : 0);
-            const h8* xq = reinterpret_cast<const h8*>(kh / KO == 0 ? k3 : v1);
+            const h8* xq = reinterpret_cast<const h8*>(kh / KO == 0 ? v2 : v3);
             qt[ks] = xq[(i * 4 + sub) * 64 + lane];
         }
     }
@@ -659,11 +644,17 @@ void prefill_attn(AttnParams P) {
     // Phase p (p = 0 .. ntile + 1): the group p % 2 runs MFMAs -- P.V of
     // tile p - 2 (its previous tile) and QK of tile p -- while the other
     // group runs tile p - 1's softmax.  Slots: K(t) in kslot[t % 4], V(t) in
-    // vslot[t % 4].  Phase p loads K(p + 2) and V(p), needed two phases
-    // later; their slots were last read in phase p - 2.  Each group runs its
-    // own straight-line phase sequence (group 0: M V M V ..., group 1:
-    // V M V M ...), both with one barrier per phase, unrolled by four so
-    // every slot is a fixed LDS object.
+    // vslot[t % 4].  Each group runs its own straight-line phase sequence
+    // (group 0: M V M V ..., group 1: V M V M ...), unrolled by four so every
+    // slot is a fixed LDS object.
+    //
+    // End of phase p: wait for this wave's direct loads (the ones issued at
+    // the end of phase p - 1: K(p + 2) and V(p), read in phase p + 2), issue
+    // the loads of phase p + 1 -- K(p + 3) and V(p + 1), into slots last read
+    // in phase p - 1 -- and pass the barrier, which makes every wave's
+    // completed loads visible.  Only one phase's loads are ever in flight at
+    // a wait, so the wait is a plain vmcnt(0) and each load still has a whole
+    // phase to land.
     const int nphase = NG == 2 ? ntile + 2 : ntile;
     auto dma = [&](int p, int R) __attribute__((always_inline)) {
         if constexpr (NG == 2) {
@@ -676,17 +667,9 @@ void prefill_attn(AttnParams P) {
             }
         }
     };
-    // End of phase p: wait for this wave's loads from phase p - 1 (the ones
-    // phase p + 1 reads), leaving phase p's own loads in flight, then the
-    // barrier makes every wave's completed loads visible.
-    const int nk = copy_count<TL::K_ELEMS * 2, kAttnWaves>(w);
-    const int nv = copy_count<TL::V_ELEMS * 2, kAttnWaves>(w);
-    auto issued = [&](int p) __attribute__((always_inline)) {
-        if constexpr (NG == 2) return (p + 2 < ntile ? nk : 0) + (p < ntile ? nv : 0);
-        else return p + 2 < ntile ? nk + nv : 0;
-    };
-    auto sync_p = [&](int p) __attribute__((always_inline)) {
-        wait_vmcnt(issued(p));
+    auto end_p = [&](int p, int R) __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(0xF70);          // vmcnt(0)
+        dma(p + 1, (R + 1) % kSlots);
         phase_barrier();
     };
     auto mphase = [&](int p, int R) __attribute__((always_inline)) {
@@ -700,35 +683,34 @@ void prefill_attn(AttnParams P) {
     if constexpr (NG == 2) {
         if (grp == 0) {
             for (int p = 0; p < nphase; p += 4) {
-                dma(p, 0); mphase(p, 0); sync_p(p);
+                mphase(p, 0); end_p(p, 0);
                 if (p + 1 >= nphase) break;
-                dma(p + 1, 1); vphase(p + 1); sync_p(p + 1);
+                vphase(p + 1); end_p(p + 1, 1);
                 if (p + 2 >= nphase) break;
-                dma(p + 2, 2); mphase(p + 2, 2); sync_p(p + 2);
+                mphase(p + 2, 2); end_p(p + 2, 2);
                 if (p + 3 >= nphase) break;
-                dma(p + 3, 3); vphase(p + 3); sync_p(p + 3);
+                vphase(p + 3); end_p(p + 3, 3);
             }
         } else {
             for (int p = 0; p < nphase; p += 4) {
-                dma(p, 0); vphase(p); sync_p(p);
+                vphase(p); end_p(p, 0);
                 if (p + 1 >= nphase) break;
-                dma(p + 1, 1); mphase(p + 1, 1); sync_p(p + 1);
+                mphase(p + 1, 1); end_p(p + 1, 1);
                 if (p + 2 >= nphase) break;
-                dma(p + 2, 2); vphase(p + 2); sync_p(p + 2);
+                vphase(p + 2); end_p(p + 2, 2);
                 if (p + 3 >= nphase) break;
-                dma(p + 3, 3); mphase(p + 3, 3); sync_p(p + 3);
+                mphase(p + 3, 3); end_p(p + 3, 3);
             }
         }
     } else {
         // One group: phase p runs tile p start to finish.
         auto whole = [&](int p, int R) __attribute__((always_inline)) {
-            dma(p, R);
             if (p < ntile) {
                 qk(kslot[R]);
                 softmax(p);
                 pv(vslot[R]);
             }
-            sync_p(p);
+            end_p(p, R);
         };
         for (int p = 0; p < nphase; p += 4) {
             whole(p, 0);
