@@ -9,8 +9,9 @@
 // two launches on the caller's stream:
 //
 // prefill_stage  one workgroup per (32 rows of a tile of KT rows, KV head);
-//                KT = 64 keys (32 for head_dim 256).  New rows (p >= pos0) get k rotated
-//                in fp32 with the reference's contraction, and k_rot / v are
+//                KT = 64 keys (32 for head_dim 256).  New rows (p >= pos0)
+//                get k rotated in fp32 with the reference's contraction, and
+//                k_rot / v are
 //                appended to the cache in its element type; rows below pos0
 //                are read back from the cache.  Every row is also written,
 //                as fp16, into a tile buffer laid out exactly as the
@@ -38,7 +39,8 @@
 //                group's waves issue MFMAs the other's run the softmax; the
 //                groups' (m, l, o) are merged at the end.  Tiles reach LDS
 //                through gfx950 direct loads (buffer_load_dwordx4 ... lds) into
-//                4-slot K and V rings, two phases ahead of use.
+//                4-slot K and V rings, issued at the end of the phase before
+//                and read two phases later.
 
 #include "pkh_internal.h"
 
