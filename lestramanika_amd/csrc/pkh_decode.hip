@@ -26,9 +26,9 @@
 // skipped on almost every tile.  At the end the row groups of a wave are
 // merged with row_ror DPP and the gfx950 permlane16/32 swaps, waves through
 // LDS, and the workgroup's (m, l, o) is either normalised into the output
-// (single-chunk sequences) or written as a split-K partial; the last work
-// item of a (sequence, KV head) to finish merges the partials in the same
-// launch.
+// (single-chunk sequences) or written as a split-K partial; the last chunk
+// of each (sequence, KV head) waits for the others' partial-ready flags and
+// merges them in the same launch.
 //
 // RoPE and append.  Every workgroup rotates its own G query heads from the
 // host-computed table row `pos` (the same sin/cos bits as the reference's
@@ -48,6 +48,7 @@ namespace {
 
 constexpr float kTau = 8.0f;   // lazy-rescale threshold (log2 units)
 constexpr int kCoherent = 16;  // buffer cache policy: sc1, device-coherent access
+constexpr int kMaxFlagPolls = 1 << 16;   // bound on the merger's wait (never reached)
 constexpr int kStream = 3;     // buffer cache policy: sc0 | nt, read-once KV stream
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -198,7 +199,7 @@ struct SplitParams {
     float* out;
     float* part_o;            // [total_chunks][H][D]
     float* part_ml;           // [total_chunks][H][2]
-    int* counters;            // [n_seqs][HK] finished chunks; zero between launches
+    int* counters;            // [HK][total chunks] partial-ready flags; zero between launches
     const float* rope_sin;
     const float* rope_cos;
     const long long* seq_slot0;
@@ -494,47 +495,71 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         }
         return;
     }
-    // Partials are written and read with device-scope atomic stores and loads,
+    // Split-K combine, fused.  The last chunk of each (sequence, KV head)
+    // merges; the others hand over their partial (max, sum, o).  Partials and
+    // flags are written and read with device-scope atomic stores and loads,
     // which go through the per-XCD L2 to the device-coherent level, so the
-    // last work item reads what the others wrote without a cache writeback
-    // or invalidate (a __threadfence here costs a full L2 writeback per
-    // workgroup).
+    // merger sees them without a cache writeback or invalidate.  A writer
+    // waits for its partial stores to complete and then sets its own flag;
+    // the merger, dispatched after every other chunk of its head (workgroups
+    // are dispatched in index order, and those chunks wait on nothing), polls
+    // the flags, merges, and clears them for the next launch.  One flag per
+    // work item replaces a shared ticket counter, whose atomics serialize
+    // when all chunks of a head finish together.
+    const bool merger = c == n_chunks - 1;
+    int* const flags = P.counters + (size_t)blockIdx.y * gridDim.x;
+    __shared__ float own_o[G * D];
+    __shared__ float own_m[G], own_l[G];
+    if (!merger) {
+#pragma unroll
+        for (int u = 0; u < OPT; u++) {
+            const int idx = (int)threadIdx.x + u * 64 * WAVES;
+            if (idx < G * D) {
+                const size_t base = (size_t)gchunk * H + head0 + idx / D;
+                __hip_atomic_store(P.part_o + base * D + idx % D, Oo[u], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                if (idx % D == 0) {
+                    __hip_atomic_store(P.part_ml + base * 2 + 0, Om[u], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(P.part_ml + base * 2 + 1, Ol[u], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_store(flags + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    // The merger keeps its own partial in LDS.
 #pragma unroll
     for (int u = 0; u < OPT; u++) {
         const int idx = (int)threadIdx.x + u * 64 * WAVES;
         if (idx < G * D) {
-            const size_t base = (size_t)gchunk * H + head0 + idx / D;
-            __hip_atomic_store(P.part_o + base * D + idx % D, Oo[u], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            if (idx % D == 0) {
-                __hip_atomic_store(P.part_ml + base * 2 + 0, Om[u], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(P.part_ml + base * 2 + 1, Ol[u], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            }
+            own_o[idx] = Oo[u];
+            if (idx % D == 0) { own_m[idx / D] = Om[u]; own_l[idx / D] = Ol[u]; }
         }
     }
-
-    // Split-K combine, fused: the last work item of (sequence, KV head) to
-    // finish merges all of its chunks.  Each thread waits for its partial
-    // stores to complete before the workgroup takes a ticket; the last one
-    // resets the count for the next launch.
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    __shared__ int last;
-    if (threadIdx.x == 0) {
-        int* cnt = P.counters + seq * HK + g;
-        const int t = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = t == n_chunks - 1;
-        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Wait for the other chunks' flags: one batch of flag loads per round.
+    // The bound only guarantees that the loop ends; every writer above sets
+    // its flag unconditionally.
+    const int cfirst = (int)blockIdx.x - c;     // this head's first chunk
+    for (int round = 0; round < kMaxFlagPolls; round++) {
+        int missing = 0;
+        for (int k = threadIdx.x; k < n_chunks - 1; k += 64 * WAVES)
+            missing |= __hip_atomic_load(flags + cfirst + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
+        if (!__syncthreads_or(missing)) break;
+        __builtin_amdgcn_s_sleep(2);
     }
-    __syncthreads();
-    if (!last) return;
-    // Final merge: the G*D outputs as float4 columns, the chunks spread over
-    // CGN thread groups so every partial load is in flight at once; the
-    // groups' online (max, sum, o) are then merged through LDS.
+    for (int k = threadIdx.x; k < n_chunks - 1; k += 64 * WAVES)
+        __hip_atomic_store(flags + cfirst + k, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int n_parts = n_chunks - 1;           // partials in memory
+    // Final merge: the G*D outputs as float4 columns, the other chunks'
+    // partials spread over CGN thread groups; the groups' online
+    // (max, sum, o) and the merger's own partial are then merged through LDS.
     constexpr int NV = G * D / 4;                       // float4 columns
     constexpr int CGN = NV >= 64 * WAVES ? 1 : 64 * WAVES / NV;
     constexpr int CPT = NV >= 64 * WAVES ? NV / (64 * WAVES) : 1;   // columns per thread
@@ -555,23 +580,44 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         const int head = head0 + h;
         float M = -INFINITY, L = 0.0f;
         float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 8
-        for (int c = cg; c < n_chunks; c += CGN) {
-            const size_t base = (size_t)(c0 + c) * H + head;
-            // 16- and 8-byte loads with the device-coherent (sc1) policy.
-            const float4 oc = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                pors, (unsigned)((base * D + (4 * col) % D) * sizeof(float)), 0, kCoherent));
-            const float2 ml = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
-                pmrs, (unsigned)(base * 2 * sizeof(float)), 0, kCoherent));
-            const float mn = fmaxf(M, ml.x);
-            const float a = (M == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(M - mn);
-            const float b = __builtin_amdgcn_exp2f(ml.x - mn);
-            L = fmaf(L, a, ml.y * b);
-            O.x = fmaf(O.x, a, oc.x * b);
-            O.y = fmaf(O.y, a, oc.y * b);
-            O.z = fmaf(O.z, a, oc.z * b);
-            O.w = fmaf(O.w, a, oc.w * b);
-            M = mn;
+        // B partials per batch, all loaded before any is used, so a batch
+        // costs one memory round trip (an unrolled online loop issues its
+        // remainder iterations one load at a time).  Slots past the last
+        // chunk reload the last one and get weight 0.
+        constexpr int B = 16;
+        for (int cb = cg; cb < n_parts; cb += CGN * B) {
+            float4 oc[B];
+            float2 ml[B];
+#pragma unroll
+            for (int i = 0; i < B; i++) {
+                const int c = min(cb + i * CGN, n_parts - 1);
+                const size_t base = (size_t)(c0 + c) * H + head;
+                // 16- and 8-byte loads with the device-coherent (sc1) policy.
+                oc[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                    pors, (unsigned)((base * D + (4 * col) % D) * sizeof(float)), 0, kCoherent));
+                ml[i] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                    pmrs, (unsigned)(base * 2 * sizeof(float)), 0, kCoherent));
+            }
+            float mb = M;
+#pragma unroll
+            for (int i = 0; i < B; i++)
+                if (cb + i * CGN < n_parts) mb = fmaxf(mb, ml[i].x);
+            const float a = (M == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(M - mb);
+            L *= a;
+            O.x *= a;
+            O.y *= a;
+            O.z *= a;
+            O.w *= a;
+#pragma unroll
+            for (int i = 0; i < B; i++) {
+                const float b = cb + i * CGN < n_parts ? __builtin_amdgcn_exp2f(ml[i].x - mb) : 0.0f;
+                L = fmaf(ml[i].y, b, L);
+                O.x = fmaf(oc[i].x, b, O.x);
+                O.y = fmaf(oc[i].y, b, O.y);
+                O.z = fmaf(oc[i].z, b, O.z);
+                O.w = fmaf(oc[i].w, b, O.w);
+            }
+            M = mb;
         }
         fo[cg][col] = O;
         if ((4 * col) % D == 0) { fm[cg][h] = M; fl[cg][h] = L; }
@@ -579,11 +625,13 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     __syncthreads();
     for (int col = threadIdx.x; col < NV; col += 64 * WAVES) {
         const int h = (4 * col) / D;
-        float M = -INFINITY;
+        float M = own_m[h];
 #pragma unroll
         for (int i = 0; i < CGN; i++) M = fmaxf(M, fm[i][h]);
-        float L = 0.0f;
-        float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const float fo_own = (own_m[h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(own_m[h] - M);
+        float L = own_l[h] * fo_own;
+        const float4 oo = *reinterpret_cast<const float4*>(&own_o[4 * col]);
+        float4 O = make_float4(oo.x * fo_own, oo.y * fo_own, oo.z * fo_own, oo.w * fo_own);
 #pragma unroll
         for (int i = 0; i < CGN; i++) {
             const float f = (fm[i][h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(fm[i][h] - M);
@@ -658,11 +706,13 @@ int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
     if (g_chunk_override > 0) {
         chunk = g_chunk_override;
     } else {
-        // About 160 work items: enough resident waves to keep HBM busy (each
-        // wave keeps DEPTH tiles in flight) while each (sequence, KV head)
-        // has few chunks for the split-K merge at the end.  Measured on the
-        // Llama-3-8B decode shape at 8K context against 64..1024 rows.
-        const long long target_items = 160;
+        // About 208 work items, at most one workgroup per CU (a CU that holds
+        // two finishes last and sets the launch time): enough resident waves
+        // to keep HBM busy (each wave keeps DEPTH tiles in flight) while each
+        // (sequence, KV head) has few chunks to merge.  Measured on the
+        // Llama-3-8B decode shape at 8K context: 208-216 items 16.7 us/layer,
+        // 160 items 17.9, 248-256 items 17.4, 264-520 items 21-23.
+        const long long target_items = 208;
         chunk = (total_rows * n_kv_heads + target_items - 1) / target_items;
         if (chunk < 2LL * tile) chunk = 2LL * tile;
         // Large batches (many sequence x head pairs) finish their merges at
@@ -714,14 +764,14 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
 
     const int total_chunks = a.total_chunks;
     if (a.max_chunks > 1) {
-        // Scratch: [part_o][part_ml]; one finished-chunk counter per
-        // (sequence, KV head) in the zero-between-launches counter array.
+        // Scratch: [part_o][part_ml]; one partial-ready flag per work item
+        // (chunk, KV head) in the zero-between-launches flag array.
         const size_t n_o = (size_t)total_chunks * H * D;
         const size_t n_ml = (size_t)total_chunks * H * 2;
         void* ws = nullptr;
         int rc = scratch_get((n_o + n_ml) * sizeof(float), &ws);
         if (rc != PKH_OK) return rc;
-        rc = counters_get((size_t)a.n_seqs * a.n_kv_heads, &P.counters);
+        rc = counters_get((size_t)total_chunks * a.n_kv_heads, &P.counters);
         if (rc != PKH_OK) return rc;
         P.part_o = reinterpret_cast<float*>(ws);
         P.part_ml = P.part_o + n_o;
