@@ -553,18 +553,29 @@ void prefill_attn(AttnParams P) {
     // kb*32 + 16tt + 8 + 4hh + (c - 4) for c >= 4: the order in which the S^T
     // accumulator holds them.  Block b + 1's V^T fragments are read while
     // block b's MFMAs run.
+    auto vfetch = [&](const _Float16* sv, int b, h8 (&dst)[NT]) __attribute__((always_inline)) {
+        const _Float16* vrow = sv + (32 * b + l32) * TL::VS + 4 * hh;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const h4 lo = *reinterpret_cast<const h4*>(vrow + 16 * t);
+            const h4 hi = *reinterpret_cast<const h4*>(vrow + 16 * t + 8);
+            dst[t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    };
+    // With two groups the first V^T block of a P.V is read at the end of the
+    // group's softmax phase before it (the tile is visible from that phase's
+    // start, and no direct load targets its slot then), so the MFMA phase
+    // does not start by waiting on LDS.
+    h8 vpre[NT];
     auto pv = [&](const _Float16* sv) __attribute__((always_inline)) {
         h8 a[2][NT];
-        auto fetch = [&](int b, h8 (&dst)[NT]) __attribute__((always_inline)) {
-            const _Float16* vrow = sv + (32 * b + l32) * TL::VS + 4 * hh;
+        auto fetch = [&](int b, h8 (&dst)[NT]) __attribute__((always_inline)) { vfetch(sv, b, dst); };
+        if constexpr (NG == 2) {
 #pragma unroll
-            for (int t = 0; t < NT; t++) {
-                const h4 lo = *reinterpret_cast<const h4*>(vrow + 16 * t);
-                const h4 hi = *reinterpret_cast<const h4*>(vrow + 16 * t + 8);
-                dst[t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            }
-        };
-        fetch(0, a[0]);
+            for (int t = 0; t < NT; t++) a[0][t] = vpre[t];
+        } else {
+            fetch(0, a[0]);
+        }
 #pragma unroll
         for (int b = 0; b < NDB; b++) {
             if (b + 1 < NDB) fetch(b + 1, a[(b + 1) & 1]);
@@ -679,27 +690,30 @@ void prefill_attn(AttnParams P) {
         __builtin_amdgcn_sched_barrier(0);   // P.V's weights die before QK's scores are born
         if (p < ntile) qk(kslot[R]);
     };
-    auto vphase = [&](int p) __attribute__((always_inline)) {
-        if (p >= 1 && p - 1 < ntile) softmax(p - 1);
+    auto vphase = [&](int p, int R) __attribute__((always_inline)) {
+        if (p >= 1 && p - 1 < ntile) {
+            softmax(p - 1);
+            vfetch(vslot[(R + 3) % kSlots], 0, vpre);   // phase p + 1's P.V of tile p - 1
+        }
     };
     if constexpr (NG == 2) {
         if (grp == 0) {
             for (int p = 0; p < nphase; p += 4) {
                 mphase(p, 0); end_p(p, 0);
                 if (p + 1 >= nphase) break;
-                vphase(p + 1); end_p(p + 1, 1);
+                vphase(p + 1, 1); end_p(p + 1, 1);
                 if (p + 2 >= nphase) break;
                 mphase(p + 2, 2); end_p(p + 2, 2);
                 if (p + 3 >= nphase) break;
-                vphase(p + 3); end_p(p + 3, 3);
+                vphase(p + 3, 3); end_p(p + 3, 3);
             }
         } else {
             for (int p = 0; p < nphase; p += 4) {
-                vphase(p); end_p(p, 0);
+                vphase(p, 0); end_p(p, 0);
                 if (p + 1 >= nphase) break;
                 mphase(p + 1, 1); end_p(p + 1, 1);
                 if (p + 2 >= nphase) break;
-                vphase(p + 2); end_p(p + 2, 2);
+                vphase(p + 2, 2); end_p(p + 2, 2);
                 if (p + 3 >= nphase) break;
                 mphase(p + 3, 3); end_p(p + 3, 3);
             }
