@@ -15,7 +15,10 @@
  *   - one host thread calls in; nothing here is reentrant;
  *   - "_async" entry points take device pointers and a hipStream_t passed as
  *     void* (NULL = the null stream), enqueue work and return; the others
- *     take host pointers and return when the result is in host memory.
+ *     take host pointers and return when the result is in host memory;
+ *   - launches on one device must not run concurrently (use one stream, or
+ *     order the streams): they share the library's device scratch -- split-K
+ *     partials and their ready flags, prefill tiles, host-pointer staging.
  *
  * Layouts (fp32 values unless stated):
  *   q   [n_heads][head_dim]           ao  [n_heads][head_dim]
