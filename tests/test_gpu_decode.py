@@ -170,6 +170,26 @@ def test_decode_chunking_is_invisible():
         assert maxerr(o, outs[0]) <= 2 * TOL_F32
 
 
+def test_decode_more_chunks_than_threads():
+    """More than 256 chunks per KV head: the merging work item polls and
+    clears the ready flags in several passes per thread and merges the
+    partials in several batches; two calls in a row must both match the
+    oracle (a flag left set would hand the second call a stale partial)."""
+    lib = pk.load()
+    H, HK, D, pos = 32, 8, 128, 12000
+    try:
+        lib.pkh_tune_decode_chunk(32)     # 376 chunks per KV head
+        for seed in (51, 52):
+            ao, ref, kv, rope = _run_case(H, HK, D, pos, 5e5, seed)
+            kv.free()
+            rope.free()
+            err = maxerr(ao, ref)
+            log(f"seed {seed}: max-abs err {err:.3e}")
+            assert err <= TOL_F32
+    finally:
+        lib.pkh_tune_decode_chunk(0)
+
+
 def test_decode_other_layers_untouched():
     H, HK, D, pos = 8, 2, 64, 100
     ao, ref, kv, rope = _run_case(H, HK, D, pos, 1e4, 21, layer=1, n_layers=3, max_seq=128)
