@@ -544,14 +544,19 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         }
     }
     // Wait for the other chunks' flags: one batch of flag loads per round.
-    // The bound only guarantees that the loop ends; every writer above sets
-    // its flag unconditionally.
+    // The bound only guarantees that the loop ends (every writer above sets
+    // its flag unconditionally); should it ever run out, the head's output
+    // is NaN rather than a merge of whatever partials had arrived.
     const int cfirst = (int)blockIdx.x - c;     // this head's first chunk
+    bool timed_out = true;
     for (int round = 0; round < kMaxFlagPolls; round++) {
         int missing = 0;
         for (int k = threadIdx.x; k < n_chunks - 1; k += 64 * WAVES)
             missing |= __hip_atomic_load(flags + cfirst + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
-        if (!__syncthreads_or(missing)) break;
+        if (!__syncthreads_or(missing)) {
+            timed_out = false;
+            break;
+        }
         __builtin_amdgcn_s_sleep(2);
     }
     for (int k = threadIdx.x; k < n_chunks - 1; k += 64 * WAVES)
@@ -642,7 +647,7 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
             O.z = fmaf(oi.z, f, O.z);
             O.w = fmaf(oi.w, f, O.w);
         }
-        const float inv = 1.0f / L;
+        const float inv = timed_out ? __builtin_nanf("") : 1.0f / L;
         *reinterpret_cast<float4*>(P.out + ((size_t)seq * H + head0 + h) * D + (4 * col) % D) =
             make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
     }
