@@ -221,10 +221,13 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     constexpr int EPL = SH::EPL, F = SH::F, LPP = SH::LPP, PPW = SH::PPW,
                   NLD = SH::NLD, S = SH::S, DEPTH = SH::DEPTH;
 
-    __shared__ float red_o[WAVES][G][D];
+    // Every row group of every wave hands its (m, l, o) to LDS at the end.
+    constexpr int NPART = WAVES * PPW;
+    static_assert(NPART * G * D * 4 <= 65536, "row-group partials fit in 64 KB of LDS");
+    __shared__ __attribute__((aligned(16))) float red_o[NPART][G][D];
     __shared__ __attribute__((aligned(16))) float q_lds[G][D];
-    __shared__ float red_m[WAVES][G];
-    __shared__ float red_l[WAVES][G];
+    __shared__ float red_m[NPART][G];
+    __shared__ float red_l[NPART][G];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -442,27 +445,27 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         }
     }
 
-    // Merge the row groups of this wave.
+    // Hand each row group's (m, l, o) to LDS: every lane writes its slice of
+    // the group's o, the group's first lane m and l.  Merging here, not with
+    // cross-lane reductions in registers, costs a few LDS reads per partial
+    // instead of three permute steps for each of the G * (F + 2) values a
+    // lane holds.
+    const int part = wave * PPW + grp;
 #pragma unroll
     for (int h = 0; h < G; h++) {
-        const float M = across_groups<LPP, true>(m[h]);
-        const float f = (m[h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[h] - M);
-        const float lh = across_groups<LPP, false>(l[h] * f);
 #pragma unroll
-        for (int e = 0; e < F; e++) acc[h][e] = across_groups<LPP, false>(acc[h][e] * f);
-        if (grp == 0) {
+        for (int i = 0; i < NLD; i++)
 #pragma unroll
-            for (int i = 0; i < NLD; i++)
-#pragma unroll
-                for (int e = 0; e < EPL; e++)
-                    red_o[wave][h][EPL * j + S * i + e] = acc[h][EPL * i + e];
-        }
-        if (lane == 0) { red_m[wave][h] = M; red_l[wave][h] = lh; }
+            for (int e = 0; e < EPL; e += 4)
+                *reinterpret_cast<float4*>(&red_o[part][h][EPL * j + S * i + e]) =
+                    make_float4(acc[h][EPL * i + e], acc[h][EPL * i + e + 1], acc[h][EPL * i + e + 2],
+                                acc[h][EPL * i + e + 3]);
+        if (j == 0) { red_m[part][h] = m[h]; red_l[part][h] = l[h]; }
     }
 
     __syncthreads();
 
-    // Merge the waves.  A sequence that fits one chunk is finished here;
+    // Merge the row groups.  A sequence that fits one chunk is finished here;
     // otherwise the work item's (max, sum, o) goes to the partial buffer.
     const int head0 = g * G;
     constexpr int OPT = (G * D + 64 * WAVES - 1) / (64 * WAVES);   // outputs per thread
@@ -473,14 +476,14 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         const int h = idx / D, d = idx % D;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < WAVES; w++) M = fmaxf(M, red_m[w][h]);
+        for (int q = 0; q < NPART; q++) M = fmaxf(M, red_m[q][h]);
         float L = 0.0f, O = 0.0f;
 #pragma unroll
-        for (int w = 0; w < WAVES; w++) {
-            const float mw = red_m[w][h];
-            const float f = (mw == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-            L = fmaf(red_l[w][h], f, L);
-            O = fmaf(red_o[w][h][d], f, O);
+        for (int q = 0; q < NPART; q++) {
+            const float mq = red_m[q][h];
+            const float f = (mq == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mq - M);
+            L = fmaf(red_l[q][h], f, L);
+            O = fmaf(red_o[q][h][d], f, O);
         }
         Om[u] = M;
         Ol[u] = L;
