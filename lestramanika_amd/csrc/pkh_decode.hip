@@ -465,8 +465,23 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
 
     __syncthreads();
 
-    // Merge the row groups.  A sequence that fits one chunk is finished here;
-    // otherwise the work item's (max, sum, o) goes to the partial buffer.
+    // Merge the row groups.  First the per-head max and each partial's
+    // weight exp2(m - max), once per (partial, head) rather than once per
+    // output; then every output is a weighted sum over the partials.  A
+    // sequence that fits one chunk is finished here; otherwise the work
+    // item's (max, sum, o) goes to the partial buffer.
+    __shared__ float red_f[NPART][G];
+    __shared__ float red_M[G];
+    for (int t = threadIdx.x; t < NPART * G; t += 64 * WAVES) {
+        const int q = t / G, h = t % G;
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < NPART; k++) M = fmaxf(M, red_m[k][h]);
+        const float mq = red_m[q][h];
+        red_f[q][h] = (mq == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mq - M);
+        if (q == 0) red_M[h] = M;
+    }
+    __syncthreads();
     const int head0 = g * G;
     constexpr int OPT = (G * D + 64 * WAVES - 1) / (64 * WAVES);   // outputs per thread
     float Om[OPT], Ol[OPT], Oo[OPT];
@@ -474,18 +489,14 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     for (int u = 0; u < OPT; u++) {
         const int idx = min((int)threadIdx.x + u * 64 * WAVES, G * D - 1);
         const int h = idx / D, d = idx % D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int q = 0; q < NPART; q++) M = fmaxf(M, red_m[q][h]);
         float L = 0.0f, O = 0.0f;
 #pragma unroll
         for (int q = 0; q < NPART; q++) {
-            const float mq = red_m[q][h];
-            const float f = (mq == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mq - M);
+            const float f = red_f[q][h];
             L = fmaf(red_l[q][h], f, L);
             O = fmaf(red_o[q][h][d], f, O);
         }
-        Om[u] = M;
+        Om[u] = red_M[h];
         Ol[u] = L;
         Oo[u] = O;
     }
