@@ -23,9 +23,9 @@
 // max m, running sum l and accumulator; m is raised only when a score exceeds
 // it by more than kTau (a wave-uniform branch that is rarely taken after the
 // first tile), so exp2(s - m) <= 2^kTau and the rescale of the accumulator is
-// skipped on almost every tile.  At the end the row groups of a wave are
-// merged with row_ror DPP and the gfx950 permlane16/32 swaps, waves through
-// LDS, and the workgroup's (m, l, o) is either normalised into the output
+// skipped on almost every tile.  At the end every row group of every wave
+// hands its (m, l, o) to LDS, where they are merged per output element, and
+// the workgroup's (m, l, o) is either normalised into the output
 // (single-chunk sequences) or written as a split-K partial; the last chunk
 // of each (sequence, KV head) waits for the others' partial-ready flags and
 // merges them in the same launch.
@@ -90,29 +90,6 @@ __device__ __forceinline__ float group_sum(float x) {
     if constexpr (LPP >= 4)  x += dpp<0x4E>(x);    // quad_perm [2,3,0,1]
     if constexpr (LPP >= 8)  x += dpp<0x141>(x);   // row_half_mirror
     if constexpr (LPP >= 16) x += dpp<0x140>(x);   // row_mirror
-    return x;
-}
-
-// Reduce over the 64/LPP row groups of a wave (lanes with equal lane % LPP);
-// every lane receives the result.  Rotations inside a 16-lane row, then the
-// gfx950 row swaps across rows.
-template <int LPP, bool IS_MAX>
-__device__ __forceinline__ float across_groups(float x) {
-    auto op = [](float a, float b) { return IS_MAX ? fmaxf(a, b) : a + b; };
-    if constexpr (LPP <= 1) x = op(x, dpp<0x121>(x));   // row_ror:1
-    if constexpr (LPP <= 2) x = op(x, dpp<0x122>(x));   // row_ror:2
-    if constexpr (LPP <= 4) x = op(x, dpp<0x124>(x));   // row_ror:4
-    if constexpr (LPP <= 8) x = op(x, dpp<0x128>(x));   // row_ror:8
-    {
-        unsigned u = __float_as_uint(x);
-        auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-        x = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
-    }
-    {
-        unsigned u = __float_as_uint(x);
-        auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-        x = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
-    }
     return x;
 }
 
