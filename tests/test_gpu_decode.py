@@ -258,3 +258,16 @@ def test_decode_split_combine_alternating_inputs():
         lib.pkh_tune_decode_chunk(0)
         kv.free()
         rope.free()
+
+
+def test_decode_interleaved_shapes():
+    """Multi-chunk decodes of five shapes, cycled twice on one device: the
+    shapes share the split-K partial buffer and ready flags under different
+    layouts and chunk counts, and every call must match the oracle -- a
+    partial written under another shape's layout, or left by an earlier
+    call, must never be merged."""
+    shapes = [(32, 8, 128, 3000), (32, 4, 64, 2500), (8, 2, 256, 1800), (8, 8, 32, 4000),
+              (32, 8, 64, 3300)]
+    for rnd in range(2):
+        for i, (H, HK, D, pos) in enumerate(shapes):
+            _check(H, HK, D, pos + rnd, 5e5, 300 + 10 * i + rnd)
