@@ -86,6 +86,18 @@ def traffic_from_profiles(workload: str):
         return None
 
 
+def cpu_model() -> str:
+    """The host CPU's model name, as /proc/cpuinfo gives it."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline_decode(K, V, q, k, v, cfg, layers, threads):
     """The oracle (the reference's OpenMP-over-heads attention, restated) on
     host copies of `layers` layers: one warm-up layer call, then one timed
@@ -221,12 +233,17 @@ def run_decode(args, cfg):
         sample_layers = min(L, args.cpu_layers)
         log(f"bench: CPU baseline (oracle, {threads} threads, {sample_layers} layers)")
         t_cpu = cpu_baseline_decode(K, V, q, k, v, cfg, sample_layers, threads)
+        t_one = cpu_baseline_decode(K, V, q, k, v, cfg, 1, 1)
         cpu = {"value": round(bpl / t_cpu / 1e9, 3), "unit": "GB/s", "cores": threads,
                "kind": "port",
                "sample": (f"one decode step over {sample_layers} layer(s) of the same workload "
                           f"({ctx} cached rows each) with the oracle's restatement of the "
                           f"reference's OpenMP-over-heads attention (oracle/pk_oracle.c)"),
-               "us_per_layer_step": round(t_cpu * 1e6, 2)}
+               "us_per_layer_step": round(t_cpu * 1e6, 2),
+               "cpu_model": cpu_model(),
+               "one_thread": {"value": round(bpl / t_one / 1e9, 3), "unit": "GB/s",
+                              "us_per_layer_step": round(t_one * 1e6, 2),
+                              "sample": "one layer of the same step on one thread"}}
 
     lib.pkh_rope_free(rp)
     result = {

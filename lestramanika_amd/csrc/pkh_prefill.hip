@@ -8,12 +8,13 @@
 // cache ends up holding the same rows.  That is what is computed here, in
 // two launches on the caller's stream:
 //
-// prefill_stage  one workgroup per (32 rows of a tile of KT rows, KV head);
-//                KT = 64 keys (32 for head_dim 256).  New rows (p >= pos0)
-//                get k rotated in fp32 with the reference's contraction, and
-//                k_rot / v are
-//                appended to the cache in its element type; rows below pos0
-//                are read back from the cache.  Every row is also written,
+// prefill_stage  one workgroup per (32 rows of a tile of KT rows, KV head),
+//                KV head fastest in dispatch order, so that neighbouring
+//                workgroups read neighbouring new rows ([n][HK][D]) and the
+//                same table rows; KT = 64 keys (32 for head_dim 256).  New
+//                rows (p >= pos0) get k rotated in fp32 with the reference's
+//                contraction, and k_rot / v are appended to the cache in its
+//                element type; rows below pos0 are read back from the cache.  Every row is also written,
 //                as fp16, into a tile buffer laid out exactly as the
 //                attention kernel keeps it in LDS: K as [key][D + kKPad] and
 //                V transposed as [d][KT + kVPad].  Rows past the last
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void prefill_stage(StageParams P) {
 
     const int tid = threadIdx.x;
     constexpr int SPLIT = TL::KT / RW;
-    const int j = blockIdx.x / SPLIT, r0 = (blockIdx.x % SPLIT) * RW, g = blockIdx.y;
+    const int j = blockIdx.y / SPLIT, r0 = (blockIdx.y % SPLIT) * RW, g = blockIdx.x;
     _Float16* tk = P.tiles + ((size_t)g * P.T + j) * TL::ELEMS;
     _Float16* tv = tk + TL::K_ELEMS;
     CT* kc = static_cast<CT*>(P.k_layer) + (size_t)g * P.stride_head;
@@ -845,6 +846,7 @@ int launch_dg(const PrefillArgs& a, hipStream_t st) {
     const long long rows = (long long)a.pos0 + a.n_tokens;
     const int T = (int)((rows + TL::KT - 1) / TL::KT);
     const int HK = a.n_kv_heads;
+    if ((long long)T * (TL::KT / StageRows<D>::N) > 65535) return PKH_ERR_ARG;   // grid y limit
     void* tiles = nullptr;
     int rc = tiles_get((size_t)HK * T * TL::BYTES, &tiles);
     if (rc != PKH_OK) return rc;
@@ -864,7 +866,10 @@ int launch_dg(const PrefillArgs& a, hipStream_t st) {
     S.HK = HK;
     S.T = T;
     S.tiles = static_cast<_Float16*>(tiles);
-    hipLaunchKernelGGL((prefill_stage<D, CT>), dim3(T * (TL::KT / StageRows<D>::N), HK), dim3(kThreads), 0, st, S);
+    // KV head fastest: measured 9.3 against 10.0 us for the Llama-3-8B
+    // 2048-row layer with the tile index fastest.
+    hipLaunchKernelGGL((prefill_stage<D, CT>), dim3(HK, T * (TL::KT / StageRows<D>::N)), dim3(kThreads), 0, st,
+                       S);
     PKH_HIP(hipGetLastError());
 
     constexpr int BM = kCols / G;
