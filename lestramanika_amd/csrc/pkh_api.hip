@@ -185,7 +185,7 @@ int copy_rows_strided(char* dev_layer, size_t stride_pos, size_t stride_head, in
 extern "C" int pkh_kv_copy_rows(const pkh_kv_t* kv, int which_v, int layer, int pos0,
                                 int n_pos, void* host, int dir) {
     if (!kv || !kv->k || !kv->v || !host || n_pos < 0) return PKH_ERR_ARG;
-    if (layer < 0 || layer >= kv->n_layers || pos0 < 0 || pos0 + n_pos > kv->max_seq)
+    if (layer < 0 || layer >= kv->n_layers || pos0 < 0 || (long long)pos0 + n_pos > kv->max_seq)
         return PKH_ERR_RANGE;
     const size_t es = elem_size(kv->dtype);
     char* base = (char*)(which_v ? kv->v : kv->k) +
@@ -517,7 +517,7 @@ extern "C" int pkh_kv_batch_copy_rows(const pkh_kv_batch_t* kvb, int which_v, in
                                       int pos0, int n_pos, void* host, int dir) {
     if (!kvb || !kvb->k || !host || n_pos < 0) return PKH_ERR_ARG;
     if (layer < 0 || layer >= kvb->n_layers || seq < 0 || seq >= kvb->n_seqs) return PKH_ERR_RANGE;
-    if (pos0 < 0 || pos0 + n_pos > kvb->max_seq[seq]) return PKH_ERR_RANGE;
+    if (pos0 < 0 || (long long)pos0 + n_pos > kvb->max_seq[seq]) return PKH_ERR_RANGE;
     const size_t es = elem_size(kvb->dtype);
     char* base = (char*)(which_v ? kvb->v : kvb->k) + (size_t)layer * kvb->layer_stride * es;
     return copy_rows_strided(base, kvb->stride_pos, kvb->stride_head, kvb->n_kv_heads,

@@ -107,6 +107,11 @@ def test_argument_checks_return_before_device_work():
                                               4, dummy, dummy, dummy, dummy)
     assert pf(0, 0) in (pk.PKH_ERR_ARG,)
     assert pf(10, 7) in (pk.PKH_ERR_RANGE, pk.PKH_ERR_ARG)
+    # row copies: a range whose end overflows int is still out of range
+    cp = lambda pos0, n: lib.pkh_kv_copy_rows(ctypes.byref(kv), 0, 0, pos0, n, dummy, 0)
+    assert cp(2**31 - 8, 16) == pk.PKH_ERR_RANGE
+    assert cp(10, 7) == pk.PKH_ERR_RANGE
+    assert cp(0, -1) == pk.PKH_ERR_ARG
     k = pk.KV()
     assert lib.pkh_kv_alloc(0, 2, 64, 16, 0, ctypes.byref(k)) == pk.PKH_ERR_ARG
     assert lib.pkh_kv_alloc(1, 2, 64, 16, 7, ctypes.byref(k)) == pk.PKH_ERR_ARG
