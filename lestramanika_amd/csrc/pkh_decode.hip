@@ -553,8 +553,6 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         }
         __builtin_amdgcn_s_sleep(2);
     }
-    for (int k = threadIdx.x; k < n_chunks - 1; k += 64 * WAVES)
-        __hip_atomic_store(flags + cfirst + k, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int n_parts = n_chunks - 1;           // partials in memory
     // Final merge: the G*D outputs as float4 columns, the other chunks'
     // partials spread over CGN thread groups; the groups' online
@@ -608,6 +606,11 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
             oc[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                 pors, (unsigned)((base * D + (4 * col) % D) * sizeof(float)), 0, kCoherent));
         }
+        // Clear the flags for the next launch once the first batch's loads
+        // are out: waits for those loads do not cover these younger stores.
+        if (b0 == 0)
+            for (int k = threadIdx.x; k < n_chunks - 1; k += 64 * WAVES)
+                __hip_atomic_store(flags + cfirst + k, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int r = 0; r < NML; r++) {
