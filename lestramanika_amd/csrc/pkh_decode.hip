@@ -497,9 +497,10 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     }
     // Split-K combine, fused.  The last chunk of each (sequence, KV head)
     // merges; the others hand over their partial (max, sum, o).  Partials and
-    // flags are written and read with device-scope atomic stores and loads,
-    // which go through the per-XCD L2 to the device-coherent level, so the
-    // merger sees them without a cache writeback or invalidate.  A writer
+    // flags are written with device-scope atomic stores and read with
+    // device-scope atomic loads or loads of the same (sc1) policy, which go
+    // through the per-XCD L2 to the device-coherent level, so the merger
+    // sees them without a cache writeback or invalidate.  A writer
     // waits for its partial stores to complete and then sets its own flag;
     // the merger, dispatched after every other chunk of its head (workgroups
     // are dispatched in index order, and those chunks wait on nothing), polls
