@@ -1,7 +1,8 @@
 /*
  * pk_oracle.c -- CPU restatement of pickle's fast-path attention block.
  *
- * TEST INFRASTRUCTURE ONLY (the checker for the HIP path; see pk_oracle.h).
+ * TEST INFRASTRUCTURE ONLY (the oracle the HIP path is checked against; see
+ * pk_oracle.h).
  *
  * Built with -ffp-contract=off so that every fused multiply-add below is an
  * explicit fmaf() (where the reference uses _mm512_fmadd_ps, or where its

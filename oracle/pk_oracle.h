@@ -1,8 +1,8 @@
 /*
  * pk_oracle.h -- CPU restatement of pickle's fast-path attention block.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP
- * attention path: it is linked or loaded only by tests/, by the smoke()
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle the HIP attention
+ * path is checked against: it is linked or loaded only by tests/, by the smoke()
  * entry point and by the CPU-baseline leg of bench.py.  Nothing in the
  * product (lestramanika_amd/) links, loads or calls it.
  *

@@ -1,8 +1,8 @@
 """numpy front end of the C oracle (oracle/liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and
-by the CPU-baseline leg of bench.py, as the checker.  The product never
-imports it.
+by the CPU-baseline leg of bench.py, to check the GPU path and to time
+the CPU baseline.  The product never imports it.
 
 Each wrapper takes and returns float32 numpy arrays in the reference's
 layouts (see pk_oracle.h for the file:line each function restates).

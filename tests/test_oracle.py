@@ -1,4 +1,4 @@
-"""CPU checks of the oracle (oracle/pk_oracle.c) -- the checker of the GPU path.
+"""CPU checks of the oracle (oracle/pk_oracle.c), against which the GPU path is checked.
 
 What pins it:
   * the reference's own outputs (tests/golden/, written by make_golden.py from
