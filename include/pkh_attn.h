@@ -18,7 +18,13 @@
  *     take host pointers and return when the result is in host memory;
  *   - launches on one device must not run concurrently (use one stream, or
  *     order the streams): they share the library's device scratch -- split-K
- *     partials and their ready flags, prefill tiles, host-pointer staging.
+ *     partials and their ready flags, prefill tiles, host-pointer staging;
+ *   - that scratch grows (hipMalloc) when a call needs more than any call
+ *     before it, and an outgrown buffer is kept, not freed, until the process
+ *     ends, so a HIP graph captured earlier stays valid.  Allocation is not
+ *     allowed inside stream capture: make one call at the largest shape
+ *     before capturing (the _async launches themselves allocate nothing
+ *     once the scratch is large enough, and record no memset).
  *
  * Layouts (fp32 values unless stated):
  *   q   [n_heads][head_dim]           ao  [n_heads][head_dim]

@@ -25,20 +25,22 @@ Buf g_staging[kMaxDevices][4];
 Buf g_tiles[kMaxDevices];
 Buf g_counters[kMaxDevices];
 
+// Buffers outgrown by a larger call.  They are never freed: a HIP graph
+// captured earlier holds their addresses and may still be replayed.  Growth
+// at least doubles, so what is retired stays below the live buffer's size.
+std::vector<void*> g_retired;
+
 int grow(Buf& b, size_t bytes, void** out) {
     if (bytes <= b.bytes && b.ptr) {
         *out = b.ptr;
         return PKH_OK;
     }
-    if (b.ptr) {
-        // Work enqueued earlier may still read the old buffer.
-        PKH_HIP(hipDeviceSynchronize());
-        PKH_HIP(hipFree(b.ptr));
-        b.ptr = nullptr;
-        b.bytes = 0;
-    }
     size_t want = bytes < 1024 ? 1024 : bytes;
-    PKH_HIP(hipMalloc(&b.ptr, want));
+    if (b.ptr && want < 2 * b.bytes) want = 2 * b.bytes;
+    void* p = nullptr;
+    PKH_HIP(hipMalloc(&p, want));
+    if (b.ptr) g_retired.push_back(b.ptr);
+    b.ptr = p;
     b.bytes = want;
     *out = b.ptr;
     return PKH_OK;

@@ -271,3 +271,76 @@ def test_decode_interleaved_shapes():
     for rnd in range(2):
         for i, (H, HK, D, pos) in enumerate(shapes):
             _check(H, HK, D, pos + rnd, 5e5, 300 + 10 * i + rnd)
+
+
+def test_decode_graph_replay_after_scratch_growth():
+    """A HIP graph captured around a decode stays valid after a later call
+    outgrows the library's split-K scratch: the outgrown partial and flag
+    buffers stay allocated, so the graph's kernels still address live memory.
+    Every replay, with eager work and synchronizations between replays,
+    matches the eager result of the same call bit for bit."""
+    import torch
+    lib = pk.load()
+    dev = torch.device("cuda")
+    H, HK, D, pos = 32, 8, 128, 3000
+    kv = DeviceKV(1, HK, D, pos + 1)
+    rope = DeviceRope(D, 5e5, pos + 1)
+    big_kv = big_rope = None
+    try:
+        kv.write(0, 0, 0, normal(61, (pos, HK, D)))
+        kv.write(1, 0, 0, normal(62, (pos, HK, D)))
+        q = torch.from_numpy(normal(63, (H, D))).to(dev)
+        k = torch.from_numpy(normal(64, (HK, D))).to(dev)
+        v = torch.from_numpy(normal(65, (HK, D))).to(dev)
+        out = torch.zeros((H, D), dtype=torch.float32, device=dev)
+
+        def call():
+            s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            rc = lib.pkh_attn_decode_async(kv.ref, rope.ref, 0, pos, H, q.data_ptr(), k.data_ptr(),
+                                           v.data_ptr(), out.data_ptr(), s)
+            assert rc == 0, rc
+
+        call()
+        torch.cuda.synchronize()
+        eager = out.clone()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                call()
+        torch.cuda.synchronize()
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), "first replay"
+        # A much larger split (1875 chunks per KV head) outgrows every buffer
+        # the earlier calls of this process sized.
+        big_pos = 60000
+        big_kv = DeviceKV(1, HK, D, big_pos + 1)
+        big_rope = DeviceRope(D, 5e5, big_pos + 1)
+        prev = lib.pkh_tune_decode_chunk(32)
+        try:
+            big = decode_host(big_kv, big_rope, 0, big_pos, normal(66, (H, D)),
+                              normal(67, (HK, D)), normal(68, (HK, D)))
+        finally:
+            lib.pkh_tune_decode_chunk(prev)
+        assert np.isfinite(big).all()
+        log("scratch grown by a 60001-row decode split into 32-row chunks")
+        for it in range(3):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {it} after growth"
+            out.zero_()
+            call()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"eager call {it} after growth"
+        log("3 replays after growth match the eager result")
+    finally:
+        kv.free()
+        rope.free()
+        if big_kv is not None:
+            big_kv.free()
+        if big_rope is not None:
+            big_rope.free()
