@@ -223,3 +223,81 @@ def test_prefill_rejects_bad_ranges():
     finally:
         kv.free()
         rope.free()
+
+
+def test_prefill_graph_replay_after_tile_growth():
+    """A HIP graph captured around a prefill (staging and attention kernels)
+    stays valid after a later, longer prefill outgrows the library's tile
+    buffer: every replay, with eager work and synchronizations between
+    replays, matches the eager result bit for bit."""
+    import torch
+    lib = pk.load()
+    dev = torch.device("cuda")
+    H, HK, D, pos0, n = 32, 8, 128, 300, 200
+    ctx_k, ctx_v, q, k, v = _inputs(H, HK, D, pos0, n, 131)
+    kv = DeviceKV(1, HK, D, pos0 + n)
+    rope = DeviceRope(D, 5e5, pos0 + n)
+    big_kv = big_rope = None
+    try:
+        kv.write(0, 0, 0, ctx_k)
+        kv.write(1, 0, 0, ctx_v)
+        tq, tk, tv = (torch.from_numpy(x).to(dev) for x in (q, k, v))
+        out = torch.zeros((n, H, D), dtype=torch.float32, device=dev)
+
+        def call():
+            s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            rc = lib.pkh_attn_prefill_async(kv.ref, rope.ref, 0, pos0, n, H, tq.data_ptr(),
+                                            tk.data_ptr(), tv.data_ptr(), out.data_ptr(), s)
+            assert rc == 0, rc
+
+        call()
+        torch.cuda.synchronize()
+        eager = out.clone()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                call()
+        torch.cuda.synchronize()
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), "first replay"
+        # An 8192-token prefill of 8 KV heads needs 128 tiles per head, more
+        # than any earlier call of this process.
+        big_n = 8192
+        big_kv = DeviceKV(1, HK, D, big_n)
+        big_rope = DeviceRope(D, 5e5, big_n)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(132)
+        bq = torch.randn((big_n, H, D), generator=gen, device=dev)
+        bk = torch.randn((big_n, HK, D), generator=gen, device=dev)
+        bv = torch.randn((big_n, HK, D), generator=gen, device=dev)
+        bo = torch.empty((big_n, H, D), dtype=torch.float32, device=dev)
+        rc = lib.pkh_attn_prefill_async(big_kv.ref, big_rope.ref, 0, 0, big_n, H, bq.data_ptr(),
+                                        bk.data_ptr(), bv.data_ptr(), bo.data_ptr(),
+                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0, rc
+        torch.cuda.synchronize()
+        assert torch.isfinite(bo).all()
+        log("tiles grown by an 8192-token prefill")
+        for it in range(3):
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {it} after growth"
+            out.zero_()
+            call()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"eager call {it} after growth"
+        log("3 replays after growth match the eager result")
+        ref, _, _ = _oracle_f32(ctx_k, ctx_v, pos0, q, k, v, rope)
+        assert maxerr(eager.cpu().numpy(), ref) <= TOL
+    finally:
+        kv.free()
+        rope.free()
+        if big_kv is not None:
+            big_kv.free()
+        if big_rope is not None:
+            big_rope.free()
