@@ -40,6 +40,13 @@
  * Supported shapes: head_dim in {16, 32, 64, 128, 256}; group size
  * n_heads / n_kv_heads in {1, 2, 4, 8} (head_dim 256: group <= 4).  Others
  * return PKH_ERR_ARG.
+ *
+ * Size limits (PKH_ERR_ARG beyond them): decode addresses one KV head's
+ * rows of one layer (of one sequence, in a batch) with 32-bit offsets, so
+ * (attended rows + 1) * stride_pos * element size must stay below 2 GiB --
+ * about 2.09M positions for an fp32 cache of head_dim 128 in the default
+ * layout.  Prefill covers at most 2,097,088 positions (pos0 + n_tokens),
+ * 1,945,184 for head_dim 256.
  */
 #ifndef PKH_ATTN_H
 #define PKH_ATTN_H

@@ -849,6 +849,8 @@ int launch_dg(const PrefillArgs& a, hipStream_t st) {
     const int T = (int)((rows + TL::KT - 1) / TL::KT);
     const int HK = a.n_kv_heads;
     if ((long long)T * (TL::KT / StageRows<D>::N) > 65535) return PKH_ERR_ARG;   // grid y limit
+    // A KV head's tiles are addressed with 32-bit signed byte offsets.
+    if ((long long)T * TL::BYTES >= (1LL << 31)) return PKH_ERR_ARG;
     void* tiles = nullptr;
     int rc = tiles_get((size_t)HK * T * TL::BYTES, &tiles);
     if (rc != PKH_OK) return rc;

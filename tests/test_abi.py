@@ -135,3 +135,28 @@ def test_tuning_hook_round_trips():
     lib = pk.load()
     prev = lib.pkh_tune_decode_chunk(512)
     assert lib.pkh_tune_decode_chunk(prev) == 512
+
+
+def test_size_limits_return_before_device_work():
+    """Calls past the 32-bit addressing limits return PKH_ERR_ARG before any
+    allocation or launch (the fake pointers are never dereferenced)."""
+    lib = pk.load()
+    dummy = ctypes.c_void_p(0x3000)
+    # Decode: (attended rows + 1) * stride_pos * 4 bytes must stay below
+    # 2 GiB -- 2,097,150 positions of an fp32 head_dim 128 cache.
+    big = 2_200_000
+    kv = _fake_kv(n_layers=1, HK=8, D=128, max_seq=big + 1)
+    kv.stride_pos, kv.stride_head = 2 * 128, (big + 1) * 2 * 128
+    rope = _fake_rope(max_seq=big + 1, half=64, filled=big + 1)
+    dec = lambda pos: lib.pkh_attn_decode_async(ctypes.byref(kv), ctypes.byref(rope), 0, pos, 32,
+                                                dummy, dummy, dummy, dummy, None)
+    assert dec(2_097_151) == pk.PKH_ERR_ARG
+    assert dec(big) == pk.PKH_ERR_ARG
+    # Prefill: 2,097,088 positions at most for head_dim 128 (launch grid),
+    # 1,945,184 for head_dim 256 (32-bit tile offsets).
+    pf = lambda kv_, rope_, H, n: lib.pkh_attn_prefill_async(
+        ctypes.byref(kv_), ctypes.byref(rope_), 0, 0, n, H, dummy, dummy, dummy, dummy, None)
+    assert pf(kv, rope, 32, 2_097_089) == pk.PKH_ERR_ARG
+    kv256 = _fake_kv(n_layers=1, HK=2, D=256, max_seq=big + 1)
+    kv256.stride_pos, kv256.stride_head = 2 * 256, (big + 1) * 2 * 256
+    assert pf(kv256, rope, 8, 1_945_185) == pk.PKH_ERR_ARG
