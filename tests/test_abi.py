@@ -160,3 +160,21 @@ def test_size_limits_return_before_device_work():
     kv256 = _fake_kv(n_layers=1, HK=2, D=256, max_seq=big + 1)
     kv256.stride_pos, kv256.stride_head = 2 * 256, (big + 1) * 2 * 256
     assert pf(kv256, rope, 8, 1_945_185) == pk.PKH_ERR_ARG
+
+
+def test_header_builds_and_links_from_c99(tmp_path):
+    """pkh_attn.h is plain C: a C99 host compiles against it with warnings as
+    errors, links -lpkh and runs the entry points that need no GPU."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    lib_dir = os.path.dirname(pk.LIB_PATH)
+    exe = str(tmp_path / "c_abi_host")
+    subprocess.run([cc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "c_abi_host.c"), "-o", exe, "-L", lib_dir,
+                    f"-Wl,-rpath,{lib_dir}", "-lpkh", "-lm"], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
+    assert "c host ok" in r.stdout
