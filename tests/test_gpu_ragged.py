@@ -193,3 +193,82 @@ def test_ragged_after_split_decode_with_fewer_counters():
         _check(32, 8, 128, [900, 3000, 1500, 64, 2200, 700, 4000, 10] * 2, 5e5, 66)
     finally:
         lib.pkh_tune_decode_chunk(0)
+
+
+def test_ragged_graph_replay_after_scratch_growth():
+    """A HIP graph of one ragged step over two layers, captured after a warm-up
+    step, stays valid after a later call outgrows the split-K scratch and
+    flags; every replay, with eager calls between, matches the eager step
+    bit for bit, and the eager step matches the oracle."""
+    import torch
+    from pkh_util import DeviceKV, decode_host, normal
+    lib = pk.load()
+    dev = torch.device("cuda")
+    H, HK, D = 32, 8, 128
+    ctx = [700, 2600, 40, 1500]
+    case = Case(H, HK, D, ctx, 5e5, 71, pk.PKH_KV_F32, n_layers=2, layer=1)
+    plan = Plan(case.kvb, ctx, H)
+    big_kv = big_rope = None
+    try:
+        n = len(ctx)
+        q = [torch.from_numpy(normal(72 + l, (n, H, D))).to(dev) for l in range(2)]
+        k = [torch.from_numpy(normal(74 + l, (n, HK, D))).to(dev) for l in range(2)]
+        v = [torch.from_numpy(normal(76 + l, (n, HK, D))).to(dev) for l in range(2)]
+        out = [torch.zeros((n, H, D), dtype=torch.float32, device=dev) for _ in range(2)]
+
+        def step():
+            s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for l in range(2):
+                rc = lib.pkh_attn_decode_batch_async(case.kvb.ref, case.rope.ref, plan.ptr, l,
+                                                     q[l].data_ptr(), k[l].data_ptr(),
+                                                     v[l].data_ptr(), out[l].data_ptr(), s)
+                assert rc == 0, rc
+
+        step()
+        torch.cuda.synchronize()
+        eager = [o.clone() for o in out]
+        for s_, p in enumerate(ctx):
+            kc, vc = case.k_rows[s_].copy(), case.v_rows[s_].copy()
+            ref, _, _ = po.decode_step(kc, vc, p, q[1][s_].cpu().numpy(), k[1][s_].cpu().numpy(),
+                                       v[1][s_].cpu().numpy(), case.rope.sin, case.rope.cos, 16)
+            assert maxerr(eager[1][s_].cpu().numpy(), ref) <= TOL_F32, s_
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                step()
+        torch.cuda.synchronize()
+        # A decode split into 5001 chunks per KV head (82 MB of partials)
+        # outgrows every buffer the earlier calls of this process sized.
+        big_pos = 80000
+        big_kv = DeviceKV(1, HK, D, big_pos + 1)
+        big_rope = DeviceRope(D, 5e5, big_pos + 1)
+        prev = lib.pkh_tune_decode_chunk(16)
+        try:
+            big = decode_host(big_kv, big_rope, 0, big_pos, normal(78, (H, D)),
+                              normal(79, (HK, D)), normal(80, (HK, D)))
+        finally:
+            lib.pkh_tune_decode_chunk(prev)
+        assert np.isfinite(big).all()
+        for it in range(3):
+            for o in out:
+                o.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            for l in range(2):
+                assert torch.equal(out[l], eager[l]), f"replay {it} layer {l}"
+            for o in out:
+                o.zero_()
+            step()
+            torch.cuda.synchronize()
+            for l in range(2):
+                assert torch.equal(out[l], eager[l]), f"eager step {it} layer {l}"
+        log("3 graph replays of a 2-layer ragged step after growth match the eager step")
+    finally:
+        plan.free()
+        case.free()
+        if big_kv is not None:
+            big_kv.free()
+        if big_rope is not None:
+            big_rope.free()
