@@ -344,3 +344,16 @@ def test_decode_graph_replay_after_scratch_growth():
             big_kv.free()
         if big_rope is not None:
             big_rope.free()
+
+
+def test_init_selects_only_existing_devices():
+    """pkh_init accepts the devices the runtime reports and rejects others
+    with PKH_ERR_ARG, leaving the current device in place."""
+    import torch
+    lib = pk.load()
+    n = torch.cuda.device_count()
+    assert lib.pkh_init(0) == pk.PKH_OK
+    assert lib.pkh_init(-1) == pk.PKH_ERR_ARG
+    assert lib.pkh_init(n) == pk.PKH_ERR_ARG
+    assert lib.pkh_init(0) == pk.PKH_OK
+    _check(8, 2, 64, 300, 1e4, 91)   # the library still decodes on device 0
