@@ -272,3 +272,13 @@ def test_ragged_graph_replay_after_scratch_growth():
             big_kv.free()
         if big_rope is not None:
             big_rope.free()
+
+
+def test_ragged_300_short_sequences():
+    """300 sequences with contexts drawn from U[0, 2000] (numpy
+    default_rng(12)), fp16 cache: thousands of work items whose sequence the
+    kernel finds by binary search over the plan's chunk starts, one-row
+    sequences among them."""
+    ctx = np.random.default_rng(12).integers(0, 2000, size=300, endpoint=True).tolist()
+    ctx[:3] = [0, 1, 2000]
+    _check(8, 2, 64, ctx, 1e4, 12, pk.PKH_KV_F16)
