@@ -26,6 +26,21 @@
  *     before capturing (the _async launches themselves allocate nothing
  *     once the scratch is large enough, and record no memset).
  *
+ * Split-K decode within one launch.  A long context is split into work
+ * items (chunks of positions); the last item of each (sequence, query-head
+ * slot) merges the others' partial results.  Two properties of the hardware
+ * are relied on:
+ *   - workgroups are dispatched in order of their index, so every item the
+ *     merger waits for has already been dispatched and waits on nothing; the
+ *     wait is bounded all the same (pkh_tune_decode_wait), and a wait that
+ *     runs out yields NaN, never a result merged from missing partials;
+ *   - a store with device-scope coherence (the partials) has reached the
+ *     device's coherence point once the storing wave's memory counter says it
+ *     completed, before the ready flag is set, and the merger's loads of the
+ *     partials use device-coherent accesses, issued after it has seen the
+ *     flags.  This is the ordering a release/acquire pair gives, without the
+ *     whole-L2 writeback a release fence would add.
+ *
  * Layouts (fp32 values unless stated):
  *   q   [n_heads][head_dim]           ao  [n_heads][head_dim]
  *   k,v [n_kv_heads][head_dim]        (the reference's state->q/k/v/ao,
@@ -259,6 +274,14 @@ int pkh_kv_batch_copy_rows(const pkh_kv_batch_t* kvb, int which_v, int layer,
 /* Decode split size: positions per work item (0 = automatic).  Values are
  * rounded up to the kernel's tile.  Returns the previous setting. */
 int pkh_tune_decode_chunk(int positions);
+
+/* Bound on the split-K merger's wait for the other work items' partials, in
+ * polling rounds (negative = the default, 65,536, which is never reached in
+ * a normal launch).  A wait that runs out writes NaN for the heads it merges
+ * and leaves no state behind that could affect a later call; 0 makes every
+ * multi-chunk decode give up at once, which tests use to force that path
+ * from the host.  Returns the previous setting. */
+int pkh_tune_decode_wait(int rounds);
 
 #ifdef __cplusplus
 }

@@ -127,6 +127,7 @@ _SIGS = {
                                          _P, _I, _P, _P, _P, _P, _P]),
     "pkh_kv_batch_copy_rows": (_I, [ctypes.POINTER(KVBatch), _I, _I, _I, _I, _I, _P, _I]),
     "pkh_tune_decode_chunk": (_I, [_I]),
+    "pkh_tune_decode_wait": (_I, [_I]),
 }
 
 _lib = None

@@ -49,7 +49,7 @@ namespace {
 
 constexpr float kTau = 8.0f;   // lazy-rescale threshold (log2 units)
 constexpr int kCoherent = 16;  // buffer cache policy: sc1, device-coherent access
-constexpr int kMaxFlagPolls = 1 << 16;   // bound on the merger's wait (never reached)
+constexpr int kMaxFlagPolls = 1 << 16;   // default bound on the merger's wait (never reached)
 constexpr int kStream = 3;     // buffer cache policy: sc0 | nt, read-once KV stream
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -178,6 +178,7 @@ struct SplitParams {
     float* part_o;            // [total_chunks][H][D]
     float* part_ml;           // [total_chunks][H][2]
     int* counters;            // [HK][total chunks] partial-ready flags; zero between launches
+    int max_polls;            // bound on the merger's flag wait, in polling rounds
     const float* rope_sin;
     const float* rope_cos;
     const long long* seq_slot0;
@@ -554,7 +555,7 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __syncthreads();
         if (threadIdx.x == 0)
-            __hip_atomic_store(flags + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(flags + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     // The merger keeps its own partial in LDS.
@@ -565,10 +566,15 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     // Wait for the other chunks' flags: one batch of flag loads per round.
     // The bound only guarantees that the loop ends (every writer above sets
     // its flag unconditionally); should it ever run out, the head's output
-    // is NaN rather than a merge of whatever partials had arrived.
+    // is NaN rather than a merge of whatever partials had arrived.  Writers
+    // add 1 to their flag and the merger subtracts 1 from every flag it
+    // waited on, whether or not the wait ran out: a writer that lands after
+    // a timed-out wait brings its flag back to 0, so the next launch (which
+    // starts after every workgroup of this one has ended) finds all flags
+    // at 0 and never takes a stale flag for its own partial.
     const int cfirst = (int)blockIdx.x - c;     // this head's first chunk
     bool timed_out = true;
-    for (int round = 0; round < kMaxFlagPolls; round++) {
+    for (int round = 0; round < P.max_polls; round++) {
         int missing = 0;
         for (int k = threadIdx.x; k < n_chunks - 1; k += 64 * WAVES)
             missing |= __hip_atomic_load(flags + cfirst + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
@@ -631,11 +637,12 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
             oc[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                 pors, (unsigned)((base * D + (4 * col) % D) * sizeof(float)), 0, kCoherent));
         }
-        // Clear the flags for the next launch once the first batch's loads
-        // are out: waits for those loads do not cover these younger stores.
+        // Return the flags to 0 for the next launch once the first batch's
+        // loads are out: waits for those loads do not cover these younger
+        // atomics.
         if (b0 == 0)
             for (int k = threadIdx.x; k < n_chunks - 1; k += 64 * WAVES)
-                __hip_atomic_store(flags + cfirst + k, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_add(flags + cfirst + k, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int r = 0; r < NML; r++) {
@@ -746,6 +753,7 @@ int decode_tile_positions(int head_dim, int group, int dtype) {
 }
 
 static int g_chunk_override = 0;
+static int g_max_polls = kMaxFlagPolls;
 
 int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
                      int n_kv_heads, int max_attend) {
@@ -801,6 +809,7 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
     P.half = a.half;
     P.chunk = a.chunk;
     P.qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
+    P.max_polls = g_max_polls;
 
     // Buffer-resource offsets are 32-bit: one sequence's rows of a layer
     // must stay below 2 GiB.
@@ -816,10 +825,11 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
         // (chunk, KV head) in the zero-between-launches flag array.
         const size_t n_o = (size_t)total_chunks * H * D;
         const size_t n_ml = (size_t)total_chunks * H * 2;
+        const size_t n_flags = (size_t)total_chunks * a.n_kv_heads;
         void* ws = nullptr;
         int rc = scratch_get((n_o + n_ml) * sizeof(float), &ws);
         if (rc != PKH_OK) return rc;
-        rc = counters_get((size_t)total_chunks * a.n_kv_heads, &P.counters);
+        rc = counters_get(n_flags, &P.counters);
         if (rc != PKH_OK) return rc;
         P.part_o = reinterpret_cast<float*>(ws);
         P.part_ml = P.part_o + n_o;
@@ -834,5 +844,11 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
 extern "C" int pkh_tune_decode_chunk(int positions) {
     const int prev = pkh::g_chunk_override;
     pkh::g_chunk_override = positions > 0 ? positions : 0;
+    return prev;
+}
+
+extern "C" int pkh_tune_decode_wait(int rounds) {
+    const int prev = pkh::g_max_polls;
+    pkh::g_max_polls = rounds >= 0 ? rounds : pkh::kMaxFlagPolls;
     return prev;
 }

@@ -357,3 +357,39 @@ def test_init_selects_only_existing_devices():
     assert lib.pkh_init(n) == pk.PKH_ERR_ARG
     assert lib.pkh_init(0) == pk.PKH_OK
     _check(8, 2, 64, 300, 1e4, 91)   # the library still decodes on device 0
+
+
+def test_decode_wait_bound_gives_nan_and_leaves_no_state():
+    """The split-K merger's bounded wait, forced to give up from the host
+    (a bound of 0 polling rounds): every head it merges comes out NaN, never
+    a merge of missing partials, and the kernel still ends normally.  The
+    next calls with the default bound match the oracle, so the timed-out
+    launch left no ready flag behind for a later launch to mistake for its
+    own partial."""
+    lib = pk.load()
+    H, HK, D, pos = 32, 8, 128, 3000
+    prev_chunk = lib.pkh_tune_decode_chunk(256)      # 12 chunks per KV head
+    prev_wait = lib.pkh_tune_decode_wait(0)
+    try:
+        ao, ref, kv, rope = _run_case(H, HK, D, pos, 5e5, 81)
+        try:
+            assert np.isnan(ao).all(), "a wait that ran out must yield NaN"
+            log("wait bound 0: all heads NaN")
+            lib.pkh_tune_decode_wait(-1)
+            q, k, v = normal(83, (H, D)), normal(84, (HK, D)), normal(85, (HK, D))
+            for it in range(2):
+                ao = decode_host(kv, rope, 0, pos, q, k, v)
+                kc = kv.read(0, 0, 0, pos + 1)
+                vc = kv.read(1, 0, 0, pos + 1)
+                kc[pos] = 0.0
+                vc[pos] = 0.0
+                ref, _, _ = po.decode_step(kc, vc, pos, q, k, v, rope.sin, rope.cos, 16)
+                err = maxerr(ao, ref)
+                log(f"  default bound, call {it}: max-abs err {err:.3e}")
+                assert err <= TOL_F32
+        finally:
+            kv.free()
+            rope.free()
+    finally:
+        lib.pkh_tune_decode_wait(prev_wait)
+        lib.pkh_tune_decode_chunk(prev_chunk)
