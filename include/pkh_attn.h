@@ -24,7 +24,8 @@
  *     ends, so a HIP graph captured earlier stays valid.  Allocation is not
  *     allowed inside stream capture: make one call at the largest shape
  *     before capturing (the _async launches themselves allocate nothing
- *     once the scratch is large enough, and record no memset).
+ *     once the scratch is large enough, and record no memset), or use
+ *     pkh_attn_decode_noalloc_async.
  *
  * Split-K decode within one launch.  A long context is split into work
  * items (chunks of positions); the last item of each (sequence, query-head
@@ -193,6 +194,23 @@ int pkh_attn_decode_async(const pkh_kv_t* kv, const pkh_rope_t* rope,
                           int layer, int pos, int n_heads, const float* d_q,
                           const float* d_k, const float* d_v, float* d_ao,
                           void* stream);
+
+/* pkh_attn_decode_async that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory during
+ * the call (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, kernels and results as
+ * pkh_attn_decode_async; the split-K partials and ready flags live in a
+ * fixed 8 MiB device array per device (64 KiB of it flags), set up by
+ * pkh_init or by the first call on a device, instead of the library's
+ * grow-only scratch.  A call whose split needs more (more than 16,384 work
+ * items, or more than 8,323,072 bytes of partials: about 500K positions at
+ * the Llama-3-8B shape) returns PKH_ERR_ARG with a line on stderr.  All
+ * calls on one device share that array: calls that overlap in time on one
+ * device race (order them on one stream). */
+int pkh_attn_decode_noalloc_async(const pkh_kv_t* kv, const pkh_rope_t* rope,
+                                  int layer, int pos, int n_heads,
+                                  const float* d_q, const float* d_k,
+                                  const float* d_v, float* d_ao, void* stream);
 
 /* ------------------------------------------------------------------ */
 /* Causal prefill: n_tokens consecutive tokens of one sequence        */

@@ -126,6 +126,8 @@ _SIGS = {
     "pkh_attn_decode_batch_async": (_I, [ctypes.POINTER(KVBatch), ctypes.POINTER(Rope),
                                          _P, _I, _P, _P, _P, _P, _P]),
     "pkh_kv_batch_copy_rows": (_I, [ctypes.POINTER(KVBatch), _I, _I, _I, _I, _I, _P, _I]),
+    "pkh_attn_decode_noalloc_async": (_I, [ctypes.POINTER(KV), ctypes.POINTER(Rope), _I, _I, _I,
+                                           _P, _P, _P, _P, _P]),
     "pkh_tune_decode_chunk": (_I, [_I]),
     "pkh_tune_decode_wait": (_I, [_I]),
 }

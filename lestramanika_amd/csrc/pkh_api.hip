@@ -105,6 +105,10 @@ extern "C" int pkh_init(int device) {
     if (device < 0 || device >= n || device >= kMaxDevices) return PKH_ERR_ARG;
     PKH_HIP(hipSetDevice(device));
     g_device = device;
+    // The no-alloc decode's fixed scratch on this device, set up once.
+    int rc = noalloc_setup(device, nullptr);
+    if (rc != PKH_OK) return rc;
+    PKH_HIP(hipStreamSynchronize(nullptr));
     return PKH_OK;
 }
 
@@ -264,7 +268,7 @@ int check_common(int head_dim, int n_heads, int n_kv_heads, const pkh_rope_t* ro
 
 int decode_checked(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer, int pos, int n_heads,
                    const float* d_q, const float* d_k, const float* d_v, float* d_ao,
-                   hipStream_t st) {
+                   hipStream_t st, bool no_alloc = false) {
     const int HK = kv->n_kv_heads, D = kv->head_dim;
     DecodeArgs a{};
     const size_t es = elem_size(kv->dtype);
@@ -290,7 +294,7 @@ int decode_checked(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer, int po
     a.rope_sin = rope->sin;
     a.rope_cos = rope->cos;
     a.half = rope->half;
-    return launch_decode(a, st);
+    return launch_decode(a, st, no_alloc);
 }
 
 bool strides_ok(size_t stride_pos, size_t stride_head, int head_dim) {
@@ -318,6 +322,17 @@ extern "C" int pkh_attn_decode_async(const pkh_kv_t* kv, const pkh_rope_t* rope,
     if (!d_q || !d_k || !d_v || !d_ao) return PKH_ERR_ARG;
     return decode_checked(kv, rope, layer, pos, n_heads, d_q, d_k, d_v, d_ao,
                           (hipStream_t)stream);
+}
+
+extern "C" int pkh_attn_decode_noalloc_async(const pkh_kv_t* kv, const pkh_rope_t* rope,
+                                             int layer, int pos, int n_heads, const float* d_q,
+                                             const float* d_k, const float* d_v, float* d_ao,
+                                             void* stream) {
+    int rc = decode_validate(kv, rope, layer, pos, n_heads);
+    if (rc != PKH_OK) return rc;
+    if (!d_q || !d_k || !d_v || !d_ao) return PKH_ERR_ARG;
+    return decode_checked(kv, rope, layer, pos, n_heads, d_q, d_k, d_v, d_ao,
+                          (hipStream_t)stream, true);
 }
 
 extern "C" int pkh_attn_decode(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer, int pos,

@@ -703,6 +703,64 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     }
 }
 
+// ---- no-alloc scratch ------------------------------------------------------
+
+__global__ void zero_words(int* p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+}  // namespace
+
+// Device scratch of pkh_attn_decode_noalloc_async: the first kNoAllocFlagBytes
+// hold the partial-ready flags (zero between launches: cleared at set-up,
+// and every launch returns the flags it used to zero), the rest the split-K
+// partials.  Each device holds its own copy until the process ends.  In host
+// code `scratch` names a host-side stand-in, not device memory: kernels and
+// copies use the address hipGetSymbolAddress returns for the current device.
+constexpr size_t kNoAllocFlagBytes = 64u << 10;
+constexpr size_t kNoAllocBytes = 8u << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+namespace {
+
+constexpr int kNoAllocDevices = 16;
+void* g_noalloc[kNoAllocDevices] = {};   // per device: the address of `scratch` there
+
+}  // namespace
+
+int noalloc_setup(int device, hipStream_t st) {
+    if (device < 0 || device >= kNoAllocDevices) return PKH_ERR_ARG;
+    if (g_noalloc[device]) return PKH_OK;
+    void* p = nullptr;
+    PKH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    // A fill kernel rather than a memset, so that a first call under stream
+    // capture records nothing a replay could get wrong.
+    hipLaunchKernelGGL(zero_words, dim3(16), dim3(256), 0, st, static_cast<int*>(p),
+                       (int)(kNoAllocFlagBytes / sizeof(int)));
+    PKH_HIP(hipGetLastError());
+    g_noalloc[device] = p;
+    return PKH_OK;
+}
+
+int noalloc_workspace(size_t part_bytes, size_t n_flags, hipStream_t st, void** part, int** flags) {
+    int dev = 0;
+    PKH_HIP(hipGetDevice(&dev));
+    if (n_flags * sizeof(int) > kNoAllocFlagBytes || part_bytes > kNoAllocBytes - kNoAllocFlagBytes) {
+        std::fprintf(stderr,
+                     "pkh: pkh_attn_decode_noalloc_async needs %zu bytes of partials and %zu flags; "
+                     "its fixed scratch holds %zu bytes and %zu flags\n",
+                     part_bytes, n_flags, kNoAllocBytes - kNoAllocFlagBytes, kNoAllocFlagBytes / sizeof(int));
+        return PKH_ERR_ARG;
+    }
+    int rc = noalloc_setup(dev, st);
+    if (rc != PKH_OK) return rc;
+    *flags = static_cast<int*>(g_noalloc[dev]);
+    *part = static_cast<char*>(g_noalloc[dev]) + kNoAllocFlagBytes;
+    return PKH_OK;
+}
+
+namespace {
+
 // ---- dispatch -------------------------------------------------------------
 
 constexpr int kWaves = 4;
@@ -785,7 +843,7 @@ int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
     return (int)chunk;
 }
 
-int launch_decode(const DecodeArgs& a, hipStream_t st) {
+int launch_decode(const DecodeArgs& a, hipStream_t st, bool no_alloc) {
     const int H = a.n_heads, D = a.head_dim;
     SplitParams P{};
     P.k_layer = a.k_layer;
@@ -827,10 +885,13 @@ int launch_decode(const DecodeArgs& a, hipStream_t st) {
         const size_t n_ml = (size_t)total_chunks * H * 2;
         const size_t n_flags = (size_t)total_chunks * a.n_kv_heads;
         void* ws = nullptr;
-        int rc = scratch_get((n_o + n_ml) * sizeof(float), &ws);
+        int rc = no_alloc ? noalloc_workspace((n_o + n_ml) * sizeof(float), n_flags, st, &ws, &P.counters)
+                          : scratch_get((n_o + n_ml) * sizeof(float), &ws);
         if (rc != PKH_OK) return rc;
-        rc = counters_get(n_flags, &P.counters);
-        if (rc != PKH_OK) return rc;
+        if (!no_alloc) {
+            rc = counters_get(n_flags, &P.counters);
+            if (rc != PKH_OK) return rc;
+        }
         P.part_o = reinterpret_cast<float*>(ws);
         P.part_ml = P.part_o + n_o;
     }

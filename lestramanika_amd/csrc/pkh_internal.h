@@ -76,7 +76,16 @@ int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
                      int n_kv_heads, int max_attend);
 int decode_tile_positions(int head_dim, int group, int dtype);
 
-int launch_decode(const DecodeArgs& a, hipStream_t stream);
+// no_alloc: take the split-K partials and flags from the library's fixed
+// device scratch (PKH_ERR_ARG when they do not fit) instead of the grow-only
+// buffers; nothing is allocated.
+int launch_decode(const DecodeArgs& a, hipStream_t stream, bool no_alloc = false);
+
+// Set up the fixed no-alloc scratch of `device` (the current device): look up
+// its address and clear its flags with a kernel on `stream`.  Once per device.
+int noalloc_setup(int device, hipStream_t stream);
+int noalloc_workspace(size_t part_bytes, size_t n_flags, hipStream_t stream, void** part,
+                      int** flags);
 
 // ---- prefill -----------------------------------------------------------
 
