@@ -51,11 +51,13 @@
  *       reference's [pos][kv_head][head_dim] (src/pickle_fast.c:1940-1942)
  *       when described so
  *   query head h reads KV head h * n_kv_heads / n_heads
- *   (src/pickle_fast.c:1963); n_heads must be a multiple of n_kv_heads.
+ *   (src/pickle_fast.c:1963), for any n_heads and n_kv_heads >= 1: groups
+ *   need not be equal or powers of two, and when n_heads < n_kv_heads some
+ *   KV heads serve no query head (their rows are still appended).
  *
- * Supported shapes: head_dim in {16, 32, 64, 128, 256}; group size
- * n_heads / n_kv_heads in {1, 2, 4, 8} (head_dim 256: group <= 4).  Others
- * return PKH_ERR_ARG.
+ * Supported shapes: head_dim 1..256 (the kernels run at the next of 16, 32,
+ * 64, 128, 256 and mask the rest), any n_heads, n_kv_heads >= 1.  head_dim
+ * above 256 and non-positive counts return PKH_ERR_ARG.
  *
  * Size limits (PKH_ERR_ARG beyond them): decode addresses one KV head's
  * rows of one layer (of one sequence, in a batch) with 32-bit offsets, so
@@ -128,8 +130,11 @@ typedef struct {
 
 /* Replaces pickle_fast_kv_alloc (src/pickle_fast.c:1793-1810): one zeroed
  * device allocation holding K and V, n_layers * max_seq * n_kv_heads *
- * head_dim elements each, in the head-major layout above.  PKH_ERR_MEMORY
- * if the device cannot hold it (the struct is zeroed). */
+ * head_dim elements each, in the head-major layout above; when head_dim is
+ * not a multiple of 8 each row is padded to the next multiple of 8 elements
+ * (stride_pos = 2 * that, v = k + that), so every row starts 16-byte
+ * aligned.  PKH_ERR_MEMORY if the device cannot hold it (the struct is
+ * zeroed). */
 int  pkh_kv_alloc(int n_layers, int n_kv_heads, int head_dim, int max_seq,
                   int dtype, pkh_kv_t* kv);
 

@@ -48,6 +48,9 @@ int grow(Buf& b, size_t bytes, void** out) {
 
 size_t elem_size(int dtype) { return dtype == PKH_KV_F16 ? 2 : 4; }
 
+// Elements per K (or V) row in the library's own cache layouts.
+size_t row_pitch(int head_dim) { return ((size_t)head_dim + 7) / 8 * 8; }
+
 bool mul_ok(size_t a, size_t b, size_t* out) {
     if (a != 0 && b > SIZE_MAX / a) return false;
     *out = a * b;
@@ -124,9 +127,12 @@ extern "C" int pkh_kv_alloc(int n_layers, int n_kv_heads, int head_dim, int max_
     std::memset(kv, 0, sizeof(*kv));
     if (n_layers <= 0 || n_kv_heads <= 0 || head_dim <= 0 || max_seq <= 0) return PKH_ERR_ARG;
     if (dtype != PKH_KV_F32 && dtype != PKH_KV_F16) return PKH_ERR_ARG;
-    // Per layer: [kv_head][pos][K row | V row].
+    // Per layer: [kv_head][pos][K row | V row], each row padded to a multiple
+    // of 8 elements (16-byte aligned rows for both element types; the padding
+    // stays zero).
+    const size_t dp = row_pitch(head_dim);
     size_t head, layer, total, bytes;
-    if (!mul_ok((size_t)max_seq, 2 * (size_t)head_dim, &head) ||
+    if (!mul_ok((size_t)max_seq, 2 * dp, &head) ||
         !mul_ok(head, (size_t)n_kv_heads, &layer) || !mul_ok(layer, (size_t)n_layers, &total) ||
         !mul_ok(total, elem_size(dtype), &bytes))
         return PKH_ERR_MEMORY;
@@ -147,10 +153,10 @@ extern "C" int pkh_kv_alloc(int n_layers, int n_kv_heads, int head_dim, int max_
     kv->k_stride_layer = layer;
     kv->v_stride_layer = layer;
     kv->k = base;
-    kv->v = (char*)base + (size_t)head_dim * elem_size(dtype);
+    kv->v = (char*)base + dp * elem_size(dtype);
     kv->dtype = dtype;
     kv->device = g_device;
-    kv->stride_pos = 2 * (size_t)head_dim;
+    kv->stride_pos = 2 * dp;
     kv->stride_head = head;
     return PKH_OK;
 }
@@ -207,8 +213,9 @@ extern "C" int pkh_kv_copy_rows(const pkh_kv_t* kv, int which_v, int layer, int 
 extern "C" int pkh_rope_alloc(int max_seq, int half, pkh_rope_t* rope) {
     if (!rope) return PKH_ERR_ARG;
     std::memset(rope, 0, sizeof(*rope));
-    if (max_seq <= 0 || half <= 0 || half > 64) return PKH_ERR_ARG;
-    const size_t bytes = (size_t)max_seq * half * sizeof(float);
+    if (max_seq <= 0 || half < 0 || half > 64) return PKH_ERR_ARG;
+    // half == 0 (head_dim 1): a table of no columns; a token allocation.
+    const size_t bytes = half ? (size_t)max_seq * half * sizeof(float) : 16;
     PKH_HIP(hipSetDevice(g_device));
     float* s = nullptr;
     float* c = nullptr;
@@ -258,8 +265,7 @@ extern "C" int pkh_rope_upload(pkh_rope_t* rope, const float* sin_tab, const flo
 namespace {
 
 int check_common(int head_dim, int n_heads, int n_kv_heads, const pkh_rope_t* rope) {
-    if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0) return PKH_ERR_ARG;
-    if (!shape_supported(head_dim, n_heads / n_kv_heads)) return PKH_ERR_ARG;
+    if (!shape_supported(head_dim, n_heads, n_kv_heads)) return PKH_ERR_ARG;
     if (!rope || !rope->sin || !rope->cos) return PKH_ERR_ARG;
     const int half = head_dim / 2 > 64 ? 64 : head_dim / 2;
     if (rope->half != half) return PKH_ERR_ARG;
@@ -284,7 +290,7 @@ int decode_checked(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer, int po
     a.pos = pos;
     a.slot0 = 0;
     const int attend_n = pos + 1;
-    a.chunk = decode_chunk_for(D, n_heads / HK, kv->dtype, attend_n, HK, attend_n);
+    a.chunk = decode_chunk_for(D, n_heads, HK, kv->dtype, attend_n, attend_n);
     a.total_chunks = (attend_n + a.chunk - 1) / a.chunk;
     a.max_chunks = a.total_chunks;
     a.q = d_q;
@@ -370,7 +376,7 @@ int prefill_validate(const pkh_kv_t* kv, const pkh_rope_t* rope, int layer, int 
     if (!strides_ok(kv->stride_pos, kv->stride_head, kv->head_dim)) return PKH_ERR_ARG;
     int rc = check_common(kv->head_dim, n_heads, kv->n_kv_heads, rope);
     if (rc != PKH_OK) return rc;
-    if (!prefill_supported(kv->head_dim, n_heads / kv->n_kv_heads, kv->dtype)) return PKH_ERR_ARG;
+    if (!prefill_supported(kv->head_dim, n_heads, kv->n_kv_heads, kv->dtype)) return PKH_ERR_ARG;
     if (n_tokens <= 0) return PKH_ERR_ARG;
     if (layer < 0 || layer >= kv->n_layers) return PKH_ERR_RANGE;
     const long long last = (long long)pos0 + n_tokens - 1;
@@ -478,10 +484,11 @@ extern "C" int pkh_kv_batch_alloc(int n_layers, int n_kv_heads, int head_dim, in
         ms[s] = max_seq[s];
         slot0[s + 1] = slot0[s] + max_seq[s];
     }
-    // Per layer: [kv_head][slot][K row | V row].
+    // Per layer: [kv_head][slot][K row | V row], rows padded as in pkh_kv_alloc.
     const size_t slots = (size_t)slot0[n_seqs];
+    const size_t dp = row_pitch(head_dim);
     size_t head, stride, total, bytes;
-    if (!mul_ok(slots, 2 * (size_t)head_dim, &head) || !mul_ok(head, (size_t)n_kv_heads, &stride) ||
+    if (!mul_ok(slots, 2 * dp, &head) || !mul_ok(head, (size_t)n_kv_heads, &stride) ||
         !mul_ok(stride, (size_t)n_layers, &total) || !mul_ok(total, elem_size(dtype), &bytes)) {
         std::free(slot0);
         std::free(ms);
@@ -511,9 +518,9 @@ extern "C" int pkh_kv_batch_alloc(int n_layers, int n_kv_heads, int head_dim, in
     kvb->slot0 = slot0;
     kvb->max_seq = ms;
     kvb->k = k;
-    kvb->v = (char*)k + (size_t)head_dim * elem_size(dtype);
+    kvb->v = (char*)k + dp * elem_size(dtype);
     kvb->d_slot0 = ds;
-    kvb->stride_pos = 2 * (size_t)head_dim;
+    kvb->stride_pos = 2 * dp;
     kvb->stride_head = head;
     return PKH_OK;
 }
@@ -547,7 +554,7 @@ extern "C" int pkh_plan_create(const pkh_kv_batch_t* kvb, const int* pos, int n_
     *out = nullptr;
     if (!kvb || !kvb->k || !pos) return PKH_ERR_ARG;
     const int HK = kvb->n_kv_heads, D = kvb->head_dim, n = kvb->n_seqs;
-    if (n_heads <= 0 || n_heads % HK != 0 || !shape_supported(D, n_heads / HK)) return PKH_ERR_ARG;
+    if (!shape_supported(D, n_heads, HK)) return PKH_ERR_ARG;
     long long rows = 0;
     int max_attend = 0, max_pos = 0;
     for (int s = 0; s < n; s++) {
@@ -556,7 +563,7 @@ extern "C" int pkh_plan_create(const pkh_kv_batch_t* kvb, const int* pos, int n_
         if (pos[s] + 1 > max_attend) max_attend = pos[s] + 1;
         if (pos[s] > max_pos) max_pos = pos[s];
     }
-    const int chunk = decode_chunk_for(D, n_heads / HK, kvb->dtype, rows, HK, max_attend);
+    const int chunk = decode_chunk_for(D, n_heads, HK, kvb->dtype, rows, max_attend);
     std::vector<int> cstart((size_t)n + 1, 0);
     int max_chunks = 0;
     for (int s = 0; s < n; s++) {

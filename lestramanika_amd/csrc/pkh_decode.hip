@@ -4,11 +4,27 @@
 // one new token over rows [0, pos]) and its multi-sequence generalisation.
 //
 // Work decomposition.  A work item is (sequence, chunk of `chunk` context
-// rows, KV head g); in a ragged batch the items of a (sequence, KV head)
+// rows, head slot y); in a ragged batch the items of a (sequence, slot)
 // instead take its row tiles round-robin.  One workgroup of WAVES wave64s
 // takes one item, so every K/V row it streams from HBM is read once and used
-// for all G = H/HK query heads of the group (the reference re-reads it G
-// times, one OpenMP thread per query head).
+// for all query heads of its slot (the reference re-reads it once per query
+// head, one OpenMP thread per head).
+//
+// Head slots.  Query head h reads KV head h*HK/H (src/pickle_fast.c:1963), so
+// KV head g serves heads [ceil(g*H/HK), ceil((g+1)*H/HK)): H/HK of them when
+// HK divides H, otherwise floor or ceil of H/HK, and none for some KV heads
+// when H < HK.  Slot y = g*nsub + sub takes up to G of those heads, starting
+// at the sub-th block of G; nsub = 1 except for groups larger than G (more
+// than 8 heads, or 4 at head_dim 256), whose slots each re-read the KV head.
+// Heads past the group's end are computed with a zero query and never
+// written.  The slot with sub == 0 appends the new row even when its KV head
+// serves no query head, as the reference appends every KV head.
+//
+// Head dimensions.  Rows are processed at a padded width D in {16, 32, 64,
+// 128, 256}; with PAD the real width Dr < D: lanes whose 16-byte load starts
+// at or past Dr load nothing (an out-of-range buffer offset returns zero
+// without a memory access), key elements past Dr are masked to zero, query
+// elements past Dr are zero, and outputs past Dr are not written.
 //
 // Register tiling.  A row of D elements is spread over LPP = D/F lanes, F
 // elements per lane, loaded with 16-byte global loads (fp32: 4 elements,
@@ -157,6 +173,16 @@ __device__ __forceinline__ void rope_block(float (&out)[EPL], const float* x, in
     }
 }
 
+// One element d of a head vector x rotated by table row (sn, cs), for rows
+// whose width or rotation half is not a multiple of 4: the same two fused
+// multiply-adds as rope_block, with scalar loads.
+__device__ __forceinline__ float rope_elem(const float* x, int d, int half, const float* sn,
+                                           const float* cs) {
+    if (d < half) return __builtin_fmaf(cs[d], x[d], -__fmul_rn(sn[d], x[d + half]));
+    if (d < 2 * half) return __builtin_fmaf(sn[d - half], x[d - half], __fmul_rn(cs[d - half], x[d]));
+    return x[d];
+}
+
 // Round the fp32 result into the cache type.  For fp16 the empty asm keeps
 // the conversion from being folded into the fused multiply-add that made x
 // (a single rounding straight to fp16); the reference rounds to fp32 first.
@@ -190,10 +216,12 @@ struct SplitParams {
     int pos;
     int n_seqs;
     int H, HK, half, chunk;
+    int Dr;                   // real head_dim (<= the kernel's padded width)
+    int nsub;                 // head slots per KV head
     float qscale;
 };
 
-template <int D, int G, typename KT, int WAVES, bool RAGGED>
+template <int D, int G, typename KT, int WAVES, bool RAGGED, bool PAD>
 __global__ __launch_bounds__(64 * WAVES)
 __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(SplitParams P) {
     using SH = Shape<D, G, KT>;
@@ -212,8 +240,13 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane % LPP;        // slot of this lane inside its row group
     const int grp = lane / LPP;      // row of the tile handled by this lane
-    const int g = blockIdx.y;        // KV head
     const int H = P.H, HK = P.HK, half = P.half;
+    const int Dr = PAD ? P.Dr : D;
+    const int y = blockIdx.y;        // head slot
+    const int g = y / P.nsub;        // its KV head
+    const int sub = y - g * P.nsub;
+    const int head0 = (g * H + HK - 1) / HK + sub * G;               // first query head
+    const int gc = min(G, (g * H + H + HK - 1) / HK - head0);        // heads of the slot
 
     int seq, c, pos, n_chunks, gchunk;
     long long slot0;
@@ -319,14 +352,19 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     };
 
     const unsigned lane_off = (unsigned)(EPL * j * sizeof(KT));
+    // With PAD, a load that starts at or past Dr gets an offset beyond every
+    // buffer extent (< 2 GiB): it returns zeros and touches no memory.
+    unsigned skip[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; i++) skip[i] = (PAD && EPL * j + S * i >= Dr) ? 0x80000000u : 0u;
     auto issue = [&](int t, uint4 (&kr)[NLD], uint4 (&vr)[NLD]) {
         const unsigned off = (unsigned)tile_row(t) * row_bytes + lane_off;
 #pragma unroll
         for (int i = 0; i < NLD; i++) {
             kr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                        krs, off + (unsigned)(S * i * sizeof(KT)), 0, kStream));
+                        krs, (off + (unsigned)(S * i * sizeof(KT))) | skip[i], 0, kStream));
             vr[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                        vrs, off + (unsigned)(S * i * sizeof(KT)), 0, kStream));
+                        vrs, (off + (unsigned)(S * i * sizeof(KT))) | skip[i], 0, kStream));
         }
     };
     auto use = [&](int t, const uint4 (&kr)[NLD], const uint4 (&vr)[NLD]) {
@@ -334,8 +372,65 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         float kf[F], vf[F];
         unpack<KT, NLD>(kr, kf);
         unpack<KT, NLD>(vr, vf);
+        if constexpr (PAD) {
+            // Key elements past Dr (a partly valid load) are masked: the
+            // zero query there must not meet a non-finite neighbour.
+#pragma unroll
+            for (int e = 0; e < F; e++)
+                if (EPL * j + S * (e / EPL) + e % EPL >= Dr) kf[e] = 0.0f;
+        }
         consume(kf, vf, p < p_end && p != pos);
     };
+
+    // The new row: rotate k for KV head g, round to the cache type, store
+    // (k_rot, v) into row pos (slot sub 0 only), and, with `fold`, fold it
+    // into the owning lane group.
+    auto new_row = [&](int r, bool fold) {   // r: row pos relative to the first row of the mapping
+        const bool mine = grp == r % PPW;
+        const bool store = mine && sub == 0;
+        float kf[F], vf[F];
+        const float* kh = P.k_new + ((size_t)seq * HK + g) * Dr;
+        const float* vh = P.v_new + ((size_t)seq * HK + g) * Dr;
+        KT* kdst = kbase + (size_t)pos * P.stride_pos;
+        KT* vdst = vbase + (size_t)pos * P.stride_pos;
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const int b = EPL * j + S * i;
+            float blk[EPL];
+            if constexpr (PAD) {
+#pragma unroll
+                for (int e = 0; e < EPL; e++) blk[e] = b + e < Dr ? rope_elem(kh, b + e, half, sn, cs) : 0.0f;
+            } else {
+                rope_block<EPL>(blk, kh, b, half, sn, cs);
+            }
+#pragma unroll
+            for (int e = 0; e < EPL; e++) {
+                const bool live = !PAD || b + e < Dr;
+                const KT kq = to_kt<KT>(blk[e]);
+                const KT vq = to_kt<KT>(live ? vh[b + e] : 0.0f);
+                if (store && live) {
+                    kdst[b + e] = kq;
+                    vdst[b + e] = vq;
+                }
+                kf[EPL * i + e] = (float)kq;
+                vf[EPL * i + e] = (float)vq;
+            }
+        }
+        if (fold) consume(kf, vf, mine);
+    };
+    // The wave whose tiles hold row pos.
+    bool owns_new;
+    if constexpr (kSweep) {
+        const int gwp = (pos / PPW) % nwh;
+        owns_new = c == gwp / WAVES && wave == gwp % WAVES;
+    } else {
+        owns_new = pos >= p_begin && pos < p_end && wave == ((pos - p_begin) / PPW) % WAVES;
+    }
+    // A slot with no query heads only appends the new row (sub 0 does).
+    if (gc <= 0) {
+        if (owns_new && sub == 0) new_row(kSweep ? pos : pos - p_begin, false);
+        return;
+    }
 
     // Main loop over this wave's tiles t = wave, wave + WAVES, ...: a ring
     // of DEPTH tiles is in flight; each consumed slot is refilled with the
@@ -354,9 +449,10 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         const int h = idx / D, d = idx % D;
         const bool lo = d < half;
         const bool hi = !lo && d < 2 * half;
-        const float* qh = P.q + ((size_t)seq * H + (size_t)g * G + h) * D;
-        qx[u] = qh[d];
-        qp[u] = qh[lo ? d + half : (hi ? d - half : d)];
+        const bool live = h < gc && d < Dr;
+        const float* qh = P.q + ((size_t)seq * H + head0 + min(h, gc - 1)) * Dr;
+        qx[u] = live ? qh[d] : 0.0f;
+        qp[u] = live ? qh[lo ? d + half : (hi ? d - half : d)] : 0.0f;
         const int ti = lo ? d : (hi ? d - half : 0);
         qs[u] = sn[ti];
         qc[u] = cs[ti];
@@ -411,40 +507,11 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         }
     }
 
-    // The new row: rotate k for KV head g, round to the cache type, store
-    // (k_rot, v) into row pos, and fold it into the owning lane group.
-    auto new_row = [&](int r) {   // r: row pos relative to the first row of the mapping
-        const bool mine = grp == r % PPW;
-        float kf[F], vf[F];
-        const float* kh = P.k_new + ((size_t)seq * HK + g) * D;
-        const float* vh = P.v_new + ((size_t)seq * HK + g) * D;
-        KT* kdst = kbase + (size_t)pos * P.stride_pos;
-        KT* vdst = vbase + (size_t)pos * P.stride_pos;
-#pragma unroll
-        for (int i = 0; i < NLD; i++) {
-            const int b = EPL * j + S * i;
-            float blk[EPL];
-            rope_block<EPL>(blk, kh, b, half, sn, cs);
-#pragma unroll
-            for (int e = 0; e < EPL; e++) {
-                const KT kq = to_kt<KT>(blk[e]);
-                const KT vq = to_kt<KT>(vh[b + e]);
-                if (mine) {
-                    kdst[b + e] = kq;
-                    vdst[b + e] = vq;
-                }
-                kf[EPL * i + e] = (float)kq;
-                vf[EPL * i + e] = (float)vq;
-            }
-        }
-        consume(kf, vf, mine);
-    };
+    // Fold the new row into the owning lane group (and append it).
     if constexpr (kSweep) {
-        const int gwp = (pos / PPW) % nwh;              // the wave whose tiles hold row pos
-        if (c == gwp / WAVES && wave == gwp % WAVES) new_row(pos);
-    } else if (pos >= p_begin && pos < p_end) {
-        const int r = pos - p_begin;
-        if (wave == (r / PPW) % WAVES) new_row(r);
+        if (owns_new) new_row(pos, true);
+    } else if (owns_new) {
+        new_row(pos - p_begin, true);
     }
 
     // Hand each row group's (m, l, o) to LDS: every lane writes its slice of
@@ -484,7 +551,6 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         if (q == 0) red_M[h] = M;
     }
     __syncthreads();
-    const int head0 = g * G;
     // Each thread finishes CW consecutive d of one head (CW = 2 where that
     // spreads the G*D outputs over every thread, else 4): one CW*4-byte LDS
     // read per partial, and its head's sum once.  Measured against one
@@ -512,11 +578,18 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         Om = red_M[oh];
     }
     if (n_chunks == 1) {
-        if (has_col) {
+        if (has_col && oh < gc) {
             fcw_t r;
 #pragma unroll
             for (int e = 0; e < CW; e++) r[e] = Oo[e] / Ol;
-            *reinterpret_cast<fcw_t*>(P.out + ((size_t)seq * H + head0 + oh) * D + od) = r;
+            float* orow = P.out + ((size_t)seq * H + head0 + oh) * Dr;
+            if constexpr (PAD) {
+#pragma unroll
+                for (int e = 0; e < CW; e++)
+                    if (od + e < Dr) orow[od + e] = r[e];
+            } else {
+                *reinterpret_cast<fcw_t*>(orow + od) = r;
+            }
         }
         return;
     }
@@ -539,7 +612,8 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     if (!merger) {
         if (has_col) {
             // 8-byte device-scope atomic stores: (o[d], o[d + 1]) pairs and (m, l).
-            const size_t base = (size_t)gchunk * H + head0 + oh;
+            // Partials are [chunk][slot][G][D].
+            const size_t base = ((size_t)gchunk * gridDim.y + y) * G + oh;
             unsigned long long* po = reinterpret_cast<unsigned long long*>(P.part_o + base * D + od);
 #pragma unroll
             for (int e = 0; e < CW; e += 2)
@@ -614,7 +688,6 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     __shared__ float2 mlb[CGN * B][G];
     const int col = col0;
     const int h = (4 * col) / D;
-    const int head = head0 + h;
     float M = -INFINITY, L = 0.0f;
     float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int b0 = 0; b0 < n_parts; b0 += CGN * B) {
@@ -625,14 +698,15 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
             const int t = min((int)threadIdx.x + r * 64 * WAVES, CGN * B * G - 1);
             const int c = min(b0 + t / G, n_parts - 1);
             mlv[r] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
-                pmrs, (unsigned)(((size_t)(c0 + c) * H + head0 + t % G) * 2 * sizeof(float)), 0, kCoherent));
+                pmrs, (unsigned)((((size_t)(c0 + c) * gridDim.y + y) * G + t % G) * 2 * sizeof(float)), 0,
+                kCoherent));
         }
         __builtin_amdgcn_sched_barrier(0);   // the pairs go out first: their wait leaves the o blocks in flight
         float4 oc[B];
 #pragma unroll
         for (int i = 0; i < B; i++) {
             const int c = min(b0 + cg + i * CGN, n_parts - 1);
-            const size_t base = (size_t)(c0 + c) * H + head;
+            const size_t base = ((size_t)(c0 + c) * gridDim.y + y) * G + h;
             // 16-byte loads with the device-coherent (sc1) policy.
             oc[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                 pors, (unsigned)((base * D + (4 * col) % D) * sizeof(float)), 0, kCoherent));
@@ -698,8 +772,19 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
             O.w = fmaf(oi.w, f, O.w);
         }
         const float inv = timed_out ? __builtin_nanf("") : 1.0f / L;
-        *reinterpret_cast<float4*>(P.out + ((size_t)seq * H + head0 + h) * D + (4 * col) % D) =
-            make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
+        if (h < gc) {
+            float* orow = P.out + ((size_t)seq * H + head0 + h) * Dr;
+            const int d = (4 * col) % D;
+            const float4 r = make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
+            if constexpr (PAD) {
+                if (d + 0 < Dr) orow[d + 0] = r.x;
+                if (d + 1 < Dr) orow[d + 1] = r.y;
+                if (d + 2 < Dr) orow[d + 2] = r.z;
+                if (d + 3 < Dr) orow[d + 3] = r.w;
+            } else {
+                *reinterpret_cast<float4*>(orow + d) = r;
+            }
+        }
     }
 }
 
@@ -766,22 +851,25 @@ namespace {
 constexpr int kWaves = 4;
 
 template <int D, int G, typename KT>
-int launch_typed(const DecodeArgs& a, const SplitParams& P, int total_chunks, hipStream_t st) {
-    dim3 grid(total_chunks, a.n_kv_heads), block(64 * kWaves);
+int launch_typed(const DecodeArgs& a, const SplitParams& P, int total_chunks, int ny, hipStream_t st) {
+    dim3 grid(total_chunks, ny), block(64 * kWaves);
     const bool ragged = a.d_chunk_start != nullptr;
-    if (ragged)
-        hipLaunchKernelGGL((decode_split<D, G, KT, kWaves, true>), grid, block, 0, st, P);
-    else
-        hipLaunchKernelGGL((decode_split<D, G, KT, kWaves, false>), grid, block, 0, st, P);
+    const bool pad = P.Dr != D;
+#define PKH_GO(R, PD) hipLaunchKernelGGL((decode_split<D, G, KT, kWaves, R, PD>), grid, block, 0, st, P)
+    if (ragged) {
+        if (pad) PKH_GO(true, true); else PKH_GO(true, false);
+    } else {
+        if (pad) PKH_GO(false, true); else PKH_GO(false, false);
+    }
+#undef PKH_GO
     PKH_HIP(hipGetLastError());
     return PKH_OK;
 }
 
 template <typename KT>
-int launch_kt(const DecodeArgs& a, const SplitParams& P, int tc, hipStream_t st) {
-    const int G = a.n_heads / a.n_kv_heads;
+int launch_kt(const DecodeArgs& a, const SplitParams& P, int tc, int ny, int DP, int G, hipStream_t st) {
 #define PKH_CASE(DD, GG) \
-    if (a.head_dim == DD && G == GG) return launch_typed<DD, GG, KT>(a, P, tc, st);
+    if (DP == DD && G == GG) return launch_typed<DD, GG, KT>(a, P, tc, ny, st);
     PKH_CASE(16, 1) PKH_CASE(16, 2) PKH_CASE(16, 4) PKH_CASE(16, 8)
     PKH_CASE(32, 1) PKH_CASE(32, 2) PKH_CASE(32, 4) PKH_CASE(32, 8)
     PKH_CASE(64, 1) PKH_CASE(64, 2) PKH_CASE(64, 4) PKH_CASE(64, 8)
@@ -791,31 +879,52 @@ int launch_kt(const DecodeArgs& a, const SplitParams& P, int tc, hipStream_t st)
     return PKH_ERR_ARG;
 }
 
+// Largest head slot of the decode kernel at padded width DP: G = 8 holds
+// 2*G*F query and accumulator registers per lane, too many at DP = 256.
+int decode_gmax(int DP) { return DP >= 256 ? 4 : 8; }
+
 }  // namespace
 
-bool shape_supported(int head_dim, int group) {
-    const bool g_ok = group == 1 || group == 2 || group == 4 || group == 8;
-    switch (head_dim) {
-        case 16: case 32: case 64: case 128: return g_ok;
-        case 256: return g_ok && group <= 4;
-        default: return false;
-    }
+int padded_head_dim(int head_dim) {
+    if (head_dim < 1 || head_dim > kMaxHeadDim) return 0;
+    int dp = 16;
+    while (dp < head_dim) dp *= 2;
+    return dp;
 }
 
-int decode_tile_positions(int head_dim, int group, int dtype) {
-    (void)group;
+HeadSlots head_slots(int n_heads, int n_kv_heads, int gmax) {
+    // KV head g serves query heads [ceil(g*H/HK), ceil((g+1)*H/HK)): at most
+    // ceil(H/HK) of them.
+    const int maxg = (n_heads + n_kv_heads - 1) / n_kv_heads;
+    int G = 1;
+    while (G < maxg && G < gmax) G *= 2;
+    return HeadSlots{G, (maxg + G - 1) / G};
+}
+
+bool shape_supported(int head_dim, int n_heads, int n_kv_heads) {
+    if (n_heads <= 0 || n_kv_heads <= 0 || padded_head_dim(head_dim) == 0) return false;
+    const int DP = padded_head_dim(head_dim);
+    const long long ny = (long long)n_kv_heads * head_slots(n_heads, n_kv_heads, decode_gmax(DP)).nsub;
+    return ny <= 65535;   // grid y
+}
+
+int decode_tile_positions(int head_dim, int dtype) {
     (void)dtype;
-    const int F = head_dim >= 256 ? 16 : 8;
-    const int lpp = head_dim / F;
+    const int DP = padded_head_dim(head_dim);
+    const int F = DP >= 256 ? 16 : 8;
+    const int lpp = DP / F;
     return (64 / lpp) * kWaves;
 }
 
 static int g_chunk_override = 0;
 static int g_max_polls = kMaxFlagPolls;
 
-int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
-                     int n_kv_heads, int max_attend) {
-    const int tile = decode_tile_positions(head_dim, group, dtype);
+int decode_chunk_for(int head_dim, int n_heads, int n_kv_heads, int dtype, long long total_rows,
+                     int max_attend) {
+    const int tile = decode_tile_positions(head_dim, dtype);
+    const int DP = padded_head_dim(head_dim);
+    // Workgroups per chunk of rows: one per head slot.
+    const long long slots = (long long)n_kv_heads * head_slots(n_heads, n_kv_heads, decode_gmax(DP)).nsub;
     long long chunk;
     if (g_chunk_override > 0) {
         chunk = g_chunk_override;
@@ -823,11 +932,11 @@ int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
         // About 208 work items, at most one workgroup per CU (a CU that holds
         // two finishes last and sets the launch time): enough resident waves
         // to keep HBM busy (each wave keeps DEPTH tiles in flight) while each
-        // (sequence, KV head) has few chunks to merge.  Measured on the
+        // (sequence, head slot) has few chunks to merge.  Measured on the
         // Llama-3-8B decode shape at 8K context: 208-216 items 16.7 us/layer,
         // 160 items 17.9, 248-256 items 17.4, 264-520 items 21-23.
         const long long target_items = 208;
-        chunk = (total_rows * n_kv_heads + target_items - 1) / target_items;
+        chunk = (total_rows * slots + target_items - 1) / target_items;
         if (chunk < 2LL * tile) chunk = 2LL * tile;
         // Large batches (many sequence x head pairs) finish their merges at
         // different times, hidden behind other items' streaming, so smaller
@@ -844,7 +953,11 @@ int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
 }
 
 int launch_decode(const DecodeArgs& a, hipStream_t st, bool no_alloc) {
-    const int H = a.n_heads, D = a.head_dim;
+    const int H = a.n_heads, HK = a.n_kv_heads;
+    const int DP = padded_head_dim(a.head_dim);
+    if (!shape_supported(a.head_dim, H, HK)) return PKH_ERR_ARG;
+    const HeadSlots hs = head_slots(H, HK, decode_gmax(DP));
+    const int ny = HK * hs.nsub;
     SplitParams P{};
     P.k_layer = a.k_layer;
     P.v_layer = a.v_layer;
@@ -863,10 +976,12 @@ int launch_decode(const DecodeArgs& a, hipStream_t st, bool no_alloc) {
     P.pos = a.pos;
     P.n_seqs = a.n_seqs;
     P.H = H;
-    P.HK = a.n_kv_heads;
+    P.HK = HK;
     P.half = a.half;
     P.chunk = a.chunk;
-    P.qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
+    P.Dr = a.head_dim;
+    P.nsub = hs.nsub;
+    P.qscale = (1.0f / sqrtf((float)a.head_dim)) * 1.4426950408889634f;
     P.max_polls = g_max_polls;
 
     // Buffer-resource offsets are 32-bit: one sequence's rows of a layer
@@ -879,11 +994,13 @@ int launch_decode(const DecodeArgs& a, hipStream_t st, bool no_alloc) {
 
     const int total_chunks = a.total_chunks;
     if (a.max_chunks > 1) {
-        // Scratch: [part_o][part_ml]; one partial-ready flag per work item
-        // (chunk, KV head) in the zero-between-launches flag array.
-        const size_t n_o = (size_t)total_chunks * H * D;
-        const size_t n_ml = (size_t)total_chunks * H * 2;
-        const size_t n_flags = (size_t)total_chunks * a.n_kv_heads;
+        // Scratch: [part_o][part_ml], partials indexed [chunk][slot][G][DP];
+        // one partial-ready flag per work item (chunk, head slot) in the
+        // zero-between-launches flag array.
+        const size_t per_chunk = (size_t)ny * hs.G;
+        const size_t n_o = (size_t)total_chunks * per_chunk * DP;
+        const size_t n_ml = (size_t)total_chunks * per_chunk * 2;
+        const size_t n_flags = (size_t)total_chunks * ny;
         void* ws = nullptr;
         int rc = no_alloc ? noalloc_workspace((n_o + n_ml) * sizeof(float), n_flags, st, &ws, &P.counters)
                           : scratch_get((n_o + n_ml) * sizeof(float), &ws);
@@ -895,8 +1012,8 @@ int launch_decode(const DecodeArgs& a, hipStream_t st, bool no_alloc) {
         P.part_o = reinterpret_cast<float*>(ws);
         P.part_ml = P.part_o + n_o;
     }
-    if (a.dtype == PKH_KV_F32) return launch_kt<float>(a, P, total_chunks, st);
-    if (a.dtype == PKH_KV_F16) return launch_kt<_Float16>(a, P, total_chunks, st);
+    if (a.dtype == PKH_KV_F32) return launch_kt<float>(a, P, total_chunks, ny, DP, hs.G, st);
+    if (a.dtype == PKH_KV_F16) return launch_kt<_Float16>(a, P, total_chunks, ny, DP, hs.G, st);
     return PKH_ERR_ARG;
 }
 

@@ -37,8 +37,25 @@ int tiles_get(size_t bytes, void** out);
 // Current device of the library.
 int current_device();
 
-// True for the (head_dim, group) pairs the kernels are instantiated for.
-bool shape_supported(int head_dim, int group);
+// Largest head_dim the kernels take (rows are processed at a padded width,
+// the next of 16, 32, 64, 128, 256).
+constexpr int kMaxHeadDim = 256;
+
+// Padded width for head_dim: 16, 32, 64, 128 or 256; 0 if unsupported.
+int padded_head_dim(int head_dim);
+
+// Query heads of one launch's workgroup ("head slot"): G in {1, 2, 4, 8}
+// heads of one KV head, nsub slots per KV head.  Query head h reads KV head
+// h*HK/H (src/pickle_fast.c:1963); gmax bounds G.
+struct HeadSlots {
+    int G;
+    int nsub;
+};
+HeadSlots head_slots(int n_heads, int n_kv_heads, int gmax);
+
+// True for every shape the decode kernels take: 1 <= head_dim <= 256, any
+// n_heads, n_kv_heads >= 1.
+bool shape_supported(int head_dim, int n_heads, int n_kv_heads);
 
 // ---- decode ------------------------------------------------------------
 
@@ -72,9 +89,9 @@ struct DecodeArgs {
 };
 
 // Positions per work item for a context of attend_n rows (tile-aligned).
-int decode_chunk_for(int head_dim, int group, int dtype, long long total_rows,
-                     int n_kv_heads, int max_attend);
-int decode_tile_positions(int head_dim, int group, int dtype);
+int decode_chunk_for(int head_dim, int n_heads, int n_kv_heads, int dtype, long long total_rows,
+                     int max_attend);
+int decode_tile_positions(int head_dim, int dtype);
 
 // no_alloc: take the split-K partials and flags from the library's fixed
 // device scratch (PKH_ERR_ARG when they do not fit) instead of the grow-only
@@ -106,7 +123,7 @@ struct PrefillArgs {
     int half;
 };
 
-bool prefill_supported(int head_dim, int group, int dtype);
+bool prefill_supported(int head_dim, int n_heads, int n_kv_heads, int dtype);
 int launch_prefill(const PrefillArgs& a, hipStream_t stream);
 
 }  // namespace pkh

@@ -35,6 +35,15 @@
 //                (the V^T reads use the same order).  Softmax runs in fp32,
 //                in log2 units (q is pre-scaled by log2(e)/sqrt(D)), with a
 //                lazily rescaled running maximum.
+//                Query heads are grouped into head slots as in decode: slot
+//                y = g*nsub + sub holds up to G heads of KV head g (query
+//                head h reads KV head h*HK/H, src/pickle_fast.c:1963), so
+//                groups of any size share the tiles; columns of heads past
+//                a group's end compute on a clamped query and are not
+//                written.  Head dimensions that are not 16, 32, 64, 128 or
+//                256 run at the next of those widths (PAD): the tiles and
+//                the query are zero past the real width and outputs there
+//                are not written; their staging uses prefill_stage_any.
 //                Two groups of 4 waves (one wave of each per SIMD) split the
 //                key tiles by parity and alternate phases, so that while one
 //                group's waves issue MFMAs the other's run the softmax; the
@@ -115,11 +124,12 @@ struct StageParams {
     void* k_layer;              // cache element type CT
     void* v_layer;
     long long stride_pos, stride_head;
-    const float* k_new;         // [n][HK][D]
+    const float* k_new;         // [n][HK][Dr]
     const float* v_new;
     const float* rope_sin;      // [max_seq][half]
     const float* rope_cos;
     int half, pos0, n, HK;
+    int Dr;                     // real head_dim
     int T;                      // tiles per head
     _Float16* tiles;            // [HK][T][Tile::ELEMS]
 };
@@ -246,17 +256,88 @@ __global__ __launch_bounds__(kThreads) void prefill_stage(StageParams P) {
     }
 }
 
+// One element d of a head vector x rotated by table row (sn, cs): the two
+// fused multiply-adds of src/pickle_fast.c:1917-1922 as compiled, with the
+// pair (d, d + half) in either order; elements past 2*half are unrotated.
+__device__ __forceinline__ float rope_at(const float* x, int d, int half, const float* sn,
+                                         const float* cs) {
+    if (d < half) return fmaf(cs[d], x[d], -(sn[d] * x[d + half]));
+    if (d < 2 * half) return fmaf(sn[d - half], x[d - half], cs[d - half] * x[d]);
+    return x[d];
+}
+
+__device__ __forceinline__ float widen(float x) { return x; }
+__device__ __forceinline__ float widen(_Float16 x) { return (float)x; }
+template <typename CT> __device__ __forceinline__ CT narrow(float x);
+template <> __device__ __forceinline__ float narrow<float>(float x) { return x; }
+template <> __device__ __forceinline__ _Float16 narrow<_Float16>(float x) { return to_f16(x); }
+
+// Staging for a real head_dim Dr below the padded width D (any Dr, any
+// rotation half): one element per thread and pass, scalar loads and stores,
+// the same rotation, cache append and tile layout as prefill_stage, zeros
+// past Dr.  Only shapes the vector staging cannot take use it.
+template <int D, typename CT>
+__global__ __launch_bounds__(kThreads) void prefill_stage_any(StageParams P) {
+    using TL = Tile<D>;
+    constexpr int RW = StageRows<D>::N;
+    constexpr int SPLIT = TL::KT / RW;
+    __shared__ __attribute__((aligned(16))) _Float16 sv[RW][D + 4];
+    const int tid = threadIdx.x;
+    const int j = blockIdx.y / SPLIT, r0 = (blockIdx.y % SPLIT) * RW, g = blockIdx.x;
+    const int Dr = P.Dr;
+    _Float16* tk = P.tiles + ((size_t)g * P.T + j) * TL::ELEMS;
+    _Float16* tv = tk + TL::K_ELEMS;
+    CT* kc = static_cast<CT*>(P.k_layer) + (size_t)g * P.stride_head;
+    CT* vc = static_cast<CT*>(P.v_layer) + (size_t)g * P.stride_head;
+    for (int idx = tid; idx < RW * D; idx += kThreads) {
+        const int rl = idx / D, d = idx % D;
+        const int p = j * TL::KT + r0 + rl;
+        float kx = 0.0f, vx = 0.0f;
+        if (d < Dr) {
+            const size_t row = (size_t)p * P.stride_pos;
+            if (p < P.pos0) {
+                kx = widen(kc[row + d]);
+                vx = widen(vc[row + d]);
+            } else if (p < P.pos0 + P.n) {
+                const size_t src = ((size_t)(p - P.pos0) * P.HK + g) * Dr;
+                kx = rope_at(P.k_new + src, d, P.half, P.rope_sin + (size_t)p * P.half,
+                             P.rope_cos + (size_t)p * P.half);
+                vx = P.v_new[src + d];
+                kc[row + d] = narrow<CT>(kx);
+                vc[row + d] = narrow<CT>(vx);
+            }
+        }
+        tk[(r0 + rl) * TL::KS + d] = to_f16(kx);
+        sv[rl][d] = to_f16(vx);
+    }
+    __syncthreads();
+    for (int u = tid; u < TL::VROWS * (RW / 8); u += kThreads) {
+        const int d = u / (RW / 8), c8 = u % (RW / 8);
+        h4 lo, hi;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            lo[i] = d < D ? sv[8 * c8 + i][d] : (_Float16)0.0f;
+            hi[i] = d < D ? sv[8 * c8 + 4 + i][d] : (_Float16)0.0f;
+        }
+        _Float16* dst = tv + d * TL::VS + r0 + 8 * c8;
+        *reinterpret_cast<h4*>(dst) = lo;
+        *reinterpret_cast<h4*>(dst + 4) = hi;
+    }
+}
+
 // ---- attention -------------------------------------------------------------
 
 struct AttnParams {
     const _Float16* tiles;      // [HK][T][Tile::ELEMS]
     int T;
-    const float* q;             // [n][H][D]
-    float* out;                 // [n][H][D]
+    const float* q;             // [n][H][Dr]
+    float* out;                 // [n][H][Dr]
     const float* rope_sin;
     const float* rope_cos;
     int half, pos0, n, H, HK, nqb;
-    float qscale;               // log2(e) / sqrt(D)
+    int Dr;                     // real head_dim
+    int nsub;                   // head slots per KV head
+    float qscale;               // log2(e) / sqrt(Dr)
 };
 
 __device__ __forceinline__ float max_halves(float x) {
@@ -332,7 +413,7 @@ template <int D> struct Groups { static constexpr int N = D >= 256 ? 1 : 2; };
 constexpr int kSlots = 4;        // K ring and V ring depth
 constexpr int kCols = 128;       // query columns per workgroup
 
-template <int D, int G>
+template <int D, int G, bool PAD>
 __global__ __launch_bounds__(256 * Groups<D>::N)
 __attribute__((amdgpu_waves_per_eu(Groups<D>::N, Groups<D>::N)))
 void prefill_attn(AttnParams P) {
@@ -360,8 +441,15 @@ void prefill_attn(AttnParams P) {
     const int lane = tid & 63, hh = lane >> 5, l32 = lane & 31;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = w >> 2, sub = w & 3;
-    const int g = blockIdx.x % P.HK;
-    const int qb = P.nqb - 1 - (int)(blockIdx.x / P.HK);      // longest first
+    const int NY = P.HK * P.nsub;                             // head slots
+    const int y = (int)(blockIdx.x % NY);
+    const int g = y / P.nsub;                                 // KV head
+    const int ysub = y - g * P.nsub;
+    const int head0 = (g * P.H + P.HK - 1) / P.HK + ysub * G;
+    const int gc = min(G, (g * P.H + P.H + P.HK - 1) / P.HK - head0);
+    if (gc <= 0) return;                                      // a KV head that serves no query head
+    const int Dr = PAD ? P.Dr : D;
+    const int qb = P.nqb - 1 - (int)(blockIdx.x / NY);        // longest first
     const int qmin_wg = P.pos0 + qb * BM;
     const int qmax = P.pos0 + min(qb * BM + BM - 1, P.n - 1);
     const int ntile = qmax / KT + 1;
@@ -392,9 +480,9 @@ void prefill_attn(AttnParams P) {
     // ks, elements d = 16ks + 8hh + [0, 8).
     const int col = 32 * sub + l32;
     const int ti = qb * BM + col / G;
-    const bool valid = ti < P.n;
-    const int tic = valid ? ti : P.n - 1;
-    const int h = g * G + col % G;
+    const bool valid = ti < P.n && col % G < gc;
+    const int tic = ti < P.n ? ti : P.n - 1;
+    const int h = head0 + min(col % G, gc - 1);
     const int qpos = P.pos0 + tic;
     // Every load of q and of its sin/cos rows is issued before any
     // arithmetic: the empty asm statements take all of them at once and hand
@@ -414,7 +502,7 @@ void prefill_attn(AttnParams P) {
         for (int e = 0; e < 8; e++) v[e] = (_Float16)(y[e] * P.qscale);
         return v;
     };
-    const float* qrow = P.q + ((size_t)tic * P.H + h) * D;
+    const float* qrow = P.q + ((size_t)tic * P.H + h) * Dr;
     const float* srow = P.rope_sin + (size_t)qpos * P.half;
     const float* crow = P.rope_cos + (size_t)qpos * P.half;
     constexpr int KH = HALF % 16 == 0 ? HALF / 16 : 1;    // k-steps holding rotated first halves
@@ -423,9 +511,22 @@ void prefill_attn(AttnParams P) {
     // other through LDS: V slots 2 (group 0's) and 3 (group 1's), whose first
     // direct loads are issued at the end of phases 1 and 2, after the phase-0
     // barrier.
-    constexpr bool kSplitQ = NG == 2 && KH >= 2 && 2 * KH == NKS;
+    constexpr bool kSplitQ = !PAD && NG == 2 && KH >= 2 && 2 * KH == NKS;
     h8 qt[NKS];
-    if constexpr (kSplitQ) {
+    if constexpr (PAD) {
+        // Any width and rotation half: element d = 16ks + 8hh + e, rotated
+        // one element at a time, zero past Dr.
+#pragma unroll
+        for (int ks = 0; ks < NKS; ks++) {
+            float y8[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int d = 16 * ks + 8 * hh + e;
+                y8[e] = d < Dr ? rope_at(qrow, d, P.half, srow, crow) : 0.0f;
+            }
+            qt[ks] = to_qt(y8);
+        }
+    } else if constexpr (kSplitQ) {
         constexpr int KO = KH / 2;
         static_assert(2 * KO * 4 * 64 * 16 <= TL::K_ELEMS * 2 && 2 * KO * 4 * 64 * 16 <= TL::V_ELEMS * 2,
                       "q exchange fits a ring slot");
@@ -816,15 +917,24 @@ void prefill_attn(AttnParams P) {
                 const int cg = 32 * sub + c;
                 const int tc = qb * BM + cg / G;
                 const int d = 32 * b + 4 * u;
-                if (tc < P.n && d < D)
-                    __builtin_nontemporal_store(__builtin_bit_cast(f32x4, o),
-                                                reinterpret_cast<f32x4*>(P.out + ((size_t)tc * P.H + g * G + cg % G) * D + d));
+                if (tc < P.n && cg % G < gc && d < Dr) {
+                    float* orow = P.out + ((size_t)tc * P.H + head0 + cg % G) * Dr;
+                    if constexpr (PAD) {
+                        const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (d + e < Dr) __builtin_nontemporal_store(ov[e], orow + d + e);
+                    } else {
+                        __builtin_nontemporal_store(__builtin_bit_cast(f32x4, o),
+                                                    reinterpret_cast<f32x4*>(orow + d));
+                    }
+                }
             }
         }
         return;
     }
     if (!valid) return;
-    float* orow = P.out + ((size_t)ti * P.H + h) * D;
+    float* orow = P.out + ((size_t)ti * P.H + h) * Dr;
 #pragma unroll
     for (int b = 0; b < NDB; b++) {
 #pragma unroll
@@ -835,7 +945,14 @@ void prefill_attn(AttnParams P) {
             o.y = acc[b][4 * r4 + 1] * inv;
             o.z = acc[b][4 * r4 + 2] * inv;
             o.w = acc[b][4 * r4 + 3] * inv;
-            if (d < D) *reinterpret_cast<float4*>(orow + d) = o;
+            if constexpr (PAD) {
+                const float ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (d + e < Dr) orow[d + e] = ov[e];
+            } else if (d < D) {
+                *reinterpret_cast<float4*>(orow + d) = o;
+            }
         }
     }
 }
@@ -843,7 +960,7 @@ void prefill_attn(AttnParams P) {
 // ---- launch ----------------------------------------------------------------
 
 template <int D, int G, typename CT>
-int launch_dg(const PrefillArgs& a, hipStream_t st) {
+int launch_dg(const PrefillArgs& a, int nsub, hipStream_t st) {
     using TL = Tile<D>;
     const long long rows = (long long)a.pos0 + a.n_tokens;
     const int T = (int)((rows + TL::KT - 1) / TL::KT);
@@ -851,10 +968,16 @@ int launch_dg(const PrefillArgs& a, hipStream_t st) {
     if ((long long)T * (TL::KT / StageRows<D>::N) > 65535) return PKH_ERR_ARG;   // grid y limit
     // A KV head's tiles are addressed with 32-bit signed byte offsets.
     if ((long long)T * TL::BYTES >= (1LL << 31)) return PKH_ERR_ARG;
+    constexpr int BM = kCols / G;
+    const long long nqb = (a.n_tokens + BM - 1) / BM;
+    if (nqb * HK * nsub > 0x7fffffffLL) return PKH_ERR_ARG;                     // grid x limit
     void* tiles = nullptr;
     int rc = tiles_get((size_t)HK * T * TL::BYTES, &tiles);
     if (rc != PKH_OK) return rc;
 
+    // The vector staging needs whole 4-element groups on both sides of the
+    // rotation half and 16-byte aligned new rows: the real width D itself.
+    const bool pad = a.head_dim != D;
     StageParams S{};
     S.k_layer = a.k_layer;
     S.v_layer = a.v_layer;
@@ -868,15 +991,18 @@ int launch_dg(const PrefillArgs& a, hipStream_t st) {
     S.pos0 = a.pos0;
     S.n = a.n_tokens;
     S.HK = HK;
+    S.Dr = a.head_dim;
     S.T = T;
     S.tiles = static_cast<_Float16*>(tiles);
     // KV head fastest: measured 9.3 against 10.0 us for the Llama-3-8B
     // 2048-row layer with the tile index fastest.
-    hipLaunchKernelGGL((prefill_stage<D, CT>), dim3(HK, T * (TL::KT / StageRows<D>::N)), dim3(kThreads), 0, st,
-                       S);
+    const dim3 sgrid(HK, T * (TL::KT / StageRows<D>::N));
+    if (pad)
+        hipLaunchKernelGGL((prefill_stage_any<D, CT>), sgrid, dim3(kThreads), 0, st, S);
+    else
+        hipLaunchKernelGGL((prefill_stage<D, CT>), sgrid, dim3(kThreads), 0, st, S);
     PKH_HIP(hipGetLastError());
 
-    constexpr int BM = kCols / G;
     AttnParams A{};
     A.tiles = static_cast<const _Float16*>(tiles);
     A.T = T;
@@ -889,27 +1015,34 @@ int launch_dg(const PrefillArgs& a, hipStream_t st) {
     A.n = a.n_tokens;
     A.H = a.n_heads;
     A.HK = HK;
-    A.nqb = (a.n_tokens + BM - 1) / BM;
-    A.qscale = (1.0f / sqrtf((float)D)) * 1.4426950408889634f;
-    hipLaunchKernelGGL((prefill_attn<D, G>), dim3(A.nqb * HK), dim3(256 * Groups<D>::N), 0, st, A);
+    A.nqb = (int)nqb;
+    A.Dr = a.head_dim;
+    A.nsub = nsub;
+    A.qscale = (1.0f / sqrtf((float)a.head_dim)) * 1.4426950408889634f;
+    const dim3 agrid((unsigned)(nqb * HK * nsub)), ablock(256 * Groups<D>::N);
+    if (pad)
+        hipLaunchKernelGGL((prefill_attn<D, G, true>), agrid, ablock, 0, st, A);
+    else
+        hipLaunchKernelGGL((prefill_attn<D, G, false>), agrid, ablock, 0, st, A);
     PKH_HIP(hipGetLastError());
     return PKH_OK;
 }
 
 template <int D, typename CT>
 int launch_d(const PrefillArgs& a, hipStream_t st) {
-    switch (a.n_heads / a.n_kv_heads) {
-        case 1: return launch_dg<D, 1, CT>(a, st);
-        case 2: return launch_dg<D, 2, CT>(a, st);
-        case 4: return launch_dg<D, 4, CT>(a, st);
-        case 8: return launch_dg<D, 8, CT>(a, st);
+    const HeadSlots hs = head_slots(a.n_heads, a.n_kv_heads, 8);
+    switch (hs.G) {
+        case 1: return launch_dg<D, 1, CT>(a, hs.nsub, st);
+        case 2: return launch_dg<D, 2, CT>(a, hs.nsub, st);
+        case 4: return launch_dg<D, 4, CT>(a, hs.nsub, st);
+        case 8: return launch_dg<D, 8, CT>(a, hs.nsub, st);
         default: return PKH_ERR_ARG;
     }
 }
 
 template <typename CT>
 int launch_ct(const PrefillArgs& a, hipStream_t st) {
-    switch (a.head_dim) {
+    switch (padded_head_dim(a.head_dim)) {
         case 16: return launch_d<16, CT>(a, st);
         case 32: return launch_d<32, CT>(a, st);
         case 64: return launch_d<64, CT>(a, st);
@@ -921,15 +1054,13 @@ int launch_ct(const PrefillArgs& a, hipStream_t st) {
 
 }  // namespace
 
-bool prefill_supported(int head_dim, int group, int dtype) {
-    const bool d_ok = head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 ||
-                      head_dim == 256;
-    const bool g_ok = group == 1 || group == 2 || group == 4 || group == 8;
-    return d_ok && g_ok && (dtype == PKH_KV_F32 || dtype == PKH_KV_F16);
+bool prefill_supported(int head_dim, int n_heads, int n_kv_heads, int dtype) {
+    return padded_head_dim(head_dim) != 0 && n_heads > 0 && n_kv_heads > 0 &&
+           (dtype == PKH_KV_F32 || dtype == PKH_KV_F16);
 }
 
 int launch_prefill(const PrefillArgs& a, hipStream_t stream) {
-    if (!prefill_supported(a.head_dim, a.n_heads / a.n_kv_heads, a.dtype)) return PKH_ERR_ARG;
+    if (!prefill_supported(a.head_dim, a.n_heads, a.n_kv_heads, a.dtype)) return PKH_ERR_ARG;
     if (a.half != rope_half_of(a.head_dim) || a.n_tokens <= 0 || a.pos0 < 0) return PKH_ERR_ARG;
     if (a.dtype == PKH_KV_F32) return launch_ct<float>(a, stream);
     return launch_ct<_Float16>(a, stream);

@@ -94,10 +94,12 @@ def test_argument_checks_return_before_device_work():
     assert dec(kv, rope, 0, 16, 4) == pk.PKH_ERR_RANGE       # pos >= max_seq
     assert dec(kv, rope, 0, -1, 4) == pk.PKH_ERR_RANGE
     assert dec(kv, _fake_rope(filled=5), 0, 5, 4) == pk.PKH_ERR_RANGE   # table not uploaded
-    assert dec(kv, rope, 0, 0, 3) == pk.PKH_ERR_ARG          # H % HK != 0
-    assert dec(kv, rope, 0, 0, 32) == pk.PKH_ERR_ARG         # group 16 unsupported
+    assert dec(kv, rope, 0, 0, 0) == pk.PKH_ERR_ARG          # no query heads
+    assert dec(kv, rope, 0, 0, -4) == pk.PKH_ERR_ARG
     assert dec(kv, _fake_rope(half=16), 0, 0, 4) == pk.PKH_ERR_ARG      # table of another D
-    assert dec(_fake_kv(D=24), _fake_rope(half=12), 0, 0, 4) == pk.PKH_ERR_ARG
+    assert dec(_fake_kv(D=24), _fake_rope(half=16), 0, 0, 4) == pk.PKH_ERR_ARG
+    assert dec(_fake_kv(D=264), _fake_rope(half=64), 0, 0, 4) == pk.PKH_ERR_ARG  # head_dim > 256
+    assert dec(_fake_kv(HK=0), rope, 0, 0, 4) == pk.PKH_ERR_ARG
     bad = _fake_kv()
     bad.stride_pos = 3                                        # strides that cannot hold a row
     assert dec(bad, rope, 0, 0, 4) == pk.PKH_ERR_ARG
@@ -118,6 +120,7 @@ def test_argument_checks_return_before_device_work():
     assert lib.pkh_kv_alloc(1, 2, 64, 16, 0, None) == pk.PKH_ERR_ARG
     r = pk.Rope()
     assert lib.pkh_rope_alloc(16, 65, ctypes.byref(r)) == pk.PKH_ERR_ARG
+    assert lib.pkh_rope_alloc(16, -1, ctypes.byref(r)) == pk.PKH_ERR_ARG
     assert lib.pkh_rope_alloc(0, 8, ctypes.byref(r)) == pk.PKH_ERR_ARG
     b = pk.KVBatch()
     ms = (ctypes.c_int * 2)(16, 0)

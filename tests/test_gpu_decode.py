@@ -77,8 +77,6 @@ def test_decode_matches_reference_outputs(path):
     """GPU decode against the compiled reference's own ao on the probe inputs."""
     z = np.load(path)
     H, HK, D, pos = (int(x) for x in z["shape"])
-    if H % HK or D % 16 or D not in (16, 32, 64, 128, 256):
-        pytest.skip("shape outside the GPU path's support (returns PKH_ERR_ARG)")
     log(f"probe {os.path.basename(path)}")
     kv = DeviceKV(1, HK, D, pos + 1)
     rope = DeviceRope(D, float(z["theta"]), pos + 1)
@@ -97,7 +95,7 @@ def test_decode_matches_reference_outputs(path):
         rope.free()
 
 
-def test_decode_unsupported_shapes_are_rejected():
+def test_decode_bad_arguments_are_rejected():
     lib = pk.load()
     kv = DeviceKV(1, 4, 16, 8)
     rope = DeviceRope(16, 1e4, 8)
@@ -105,9 +103,9 @@ def test_decode_unsupported_shapes_are_rejected():
         q = np.zeros((6, 16), np.float32)
         k = np.zeros((4, 16), np.float32)
         ao = np.zeros_like(q)
-        rc = lib.pkh_attn_decode(kv.ref, rope.ref, 0, 3, 6, q.ctypes.data, k.ctypes.data,
+        rc = lib.pkh_attn_decode(kv.ref, rope.ref, 0, 3, 0, q.ctypes.data, k.ctypes.data,
                                  k.ctypes.data, ao.ctypes.data)
-        assert rc == pk.PKH_ERR_ARG
+        assert rc == pk.PKH_ERR_ARG          # no query heads
         rc = lib.pkh_attn_decode(kv.ref, rope.ref, 0, 8, 8, q.ctypes.data, k.ctypes.data,
                                  k.ctypes.data, ao.ctypes.data)
         assert rc == pk.PKH_ERR_RANGE
@@ -130,8 +128,6 @@ def test_decode_llama3_8b_shape_ctx8192():
 @pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("G", [1, 2, 4, 8])
 def test_decode_shape_sweep(D, G):
-    if D == 256 and G == 8:
-        pytest.skip("head_dim 256 supports groups up to 4")
     HK = 2
     for pos in (0, 1, 63, 130, 1031):
         _check(G * HK, HK, D, pos, 1e4, 100 + D + G + pos)

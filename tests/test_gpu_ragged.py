@@ -159,8 +159,8 @@ def test_ragged_rejects_bad_plans():
         ptr = ctypes.c_void_p()
         assert lib.pkh_plan_create(kvb.ref, (ctypes.c_int * 2)(8, 3), 4,
                                    ctypes.byref(ptr)) == pk.PKH_ERR_RANGE   # pos >= max_seq
-        assert lib.pkh_plan_create(kvb.ref, (ctypes.c_int * 2)(1, 3), 3,
-                                   ctypes.byref(ptr)) == pk.PKH_ERR_ARG     # H % HK
+        assert lib.pkh_plan_create(kvb.ref, (ctypes.c_int * 2)(1, 3), 0,
+                                   ctypes.byref(ptr)) == pk.PKH_ERR_ARG     # no query heads
         assert lib.pkh_kv_batch_copy_rows(kvb.ref, 0, 0, 2, 0, 1, ctypes.c_void_p(1),
                                           0) == pk.PKH_ERR_RANGE              # no sequence 2
     finally:
