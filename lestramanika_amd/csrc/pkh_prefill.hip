@@ -54,6 +54,7 @@
 
 #include "pkh_internal.h"
 
+#include <algorithm>
 #include <cmath>
 #include <utility>
 
@@ -132,7 +133,168 @@ struct StageParams {
     int Dr;                     // real head_dim
     int T;                      // tiles per head
     _Float16* tiles;            // [HK][T][Tile::ELEMS]
+    // Rows at positions below kExactKeys, computed in fp32 by extra
+    // workgroups of this launch (grid rows past the staging ones).
+    const float* q;             // [n][H][Dr]
+    float* out;                 // [n][H][Dr]
+    int H, Gs, nsub;            // query heads; head slots as in prefill_attn
+    float qscale;               // log2(e) / sqrt(Dr)
 };
+
+// One element d of a head vector x rotated by table row (sn, cs): the two
+// fused multiply-adds of src/pickle_fast.c:1917-1922 as compiled, with the
+// pair (d, d + half) in either order; elements past 2*half are unrotated.
+// Branch-free: the four loads do not depend on which case applies, so a
+// caller's unrolled loop issues all of them before any arithmetic.
+__device__ __forceinline__ float rope_at(const float* x, int d, int half, const float* sn,
+                                         const float* cs) {
+    const bool lo = d < half, hi = !lo && d < 2 * half;
+    const int pd = lo ? d + half : (hi ? d - half : d);
+    const int ti = lo ? d : (hi ? d - half : 0);
+    const float xd = x[d], xp = x[pd], s = sn[ti], c = cs[ti];
+    const float r_lo = fmaf(c, xd, -(s * xp));
+    const float r_hi = fmaf(s, xp, c * xd);
+    return lo ? r_lo : (hi ? r_hi : xd);
+}
+
+__device__ __forceinline__ float widen(float x) { return x; }
+__device__ __forceinline__ float widen(_Float16 x) { return (float)x; }
+template <typename CT> __device__ __forceinline__ CT narrow(float x);
+template <> __device__ __forceinline__ float narrow<float>(float x) { return x; }
+template <> __device__ __forceinline__ _Float16 narrow<_Float16>(float x) { return to_f16(x); }
+
+// Rows at positions below kExactKeys (at most that many keys) are computed
+// in fp32 by extra workgroups of prefill_stage, one per (row, head slot),
+// which run beside the staging workgroups (the launch is bound by memory
+// traffic, not by the VALU); prefill_attn leaves those rows alone.  fp16
+// rounding costs such a row
+// the most: with one key its output is v rounded to fp16, up to 2^-9 ~ 1.95e-3
+// for |v| in [4, 8), while over longer ranges the roundings average out.
+// Measured over 20 seeds of a 2048-token Llama-3-8B-shape prompt (fp16 for
+// every row): worst 1.94e-3, all in rows 0-11; emulated by number of keys,
+// 1.9e-3 below 8 keys, 1.35e-3 for 8-15, 1.1e-3 for 16-31, under 1e-3 above.
+constexpr int kExactKeys = 16;
+
+// The reference's decode step (src/pickle_fast.c:1946-2094) for row r and
+// the query heads of head slot y, in fp32: q rotated with the reference's
+// contraction and scaled, dot products with the row's <= kExactKeys keys,
+// exact max, exp2, weighted sum of the values.  Keys below pos0 come from
+// the cache; the row's new keys are rotated from the inputs exactly as the
+// staging workgroups rotate them (and rounded to the cache type), since
+// those are writing the cache concurrently.  Every load is unconditional
+// (indices clamped into range, results selected), so each step is one
+// memory round trip.  lds: kExactLds floats.
+constexpr int kExactSlot = 8;                                 // largest head slot
+template <int D> struct ExactLds {
+    static constexpr int Q = kExactSlot * D, K = kExactKeys * (D + 1), V = kExactKeys * D,
+                         S = kExactSlot * kExactKeys;
+    static constexpr int N = Q + K + V + S;
+};
+
+template <int D, typename CT, int NT>
+__device__ void exact_row(const StageParams& P, int e, float* lds) {
+    const int NY = P.HK * P.nsub;
+    const int r = e / NY, y = e - (e / NY) * NY;
+    const int g = y / P.nsub, ysub = y - g * P.nsub;
+    const int head0 = (g * P.H + P.HK - 1) / P.HK + ysub * P.Gs;
+    const int gc = min(P.Gs, (g * P.H + P.H + P.HK - 1) / P.HK - head0);
+    if (gc <= 0) return;
+    float* qs = lds;
+    float* ks = qs + ExactLds<D>::Q;
+    float* vs = ks + ExactLds<D>::K;
+    float* sc = vs + ExactLds<D>::V;
+    const int Dr = P.Dr, half = P.half;
+    const int pos = P.pos0 + r, nk = pos + 1;
+    const int tid = threadIdx.x;
+    constexpr int NQ = (kExactSlot * D + NT - 1) / NT, NKV = (kExactKeys * D + NT - 1) / NT;
+    float qv[NQ], kl[NKV], vl[NKV];
+    {
+        const float* sn = P.rope_sin + (size_t)pos * half;
+        const float* cs = P.rope_cos + (size_t)pos * half;
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            const int idx = min(tid + i * NT, P.Gs * D - 1), h = idx / D, d = idx % D;
+            const float* qrow = P.q + ((size_t)r * P.H + head0 + min(h, gc - 1)) * Dr;
+            qv[i] = rope_at(qrow, min(d, Dr - 1), half, sn, cs) * P.qscale;
+        }
+    }
+    const CT* kc = static_cast<const CT*>(P.k_layer) + (size_t)g * P.stride_head;
+    const CT* vc = static_cast<const CT*>(P.v_layer) + (size_t)g * P.stride_head;
+    // A prompt from position 0 (the usual case, a uniform branch) has only
+    // new keys and skips the cache loads.
+    const bool from_cache = P.pos0 > 0;
+#pragma unroll
+    for (int i = 0; i < NKV; i++) {
+        const int idx = min(tid + i * NT, kExactKeys * D - 1), key = min(idx / D, nk - 1);
+        const int d = min(idx % D, Dr - 1);
+        const int knew = max(key - P.pos0, 0);
+        const size_t src = ((size_t)knew * P.HK + g) * Dr;
+        const float krot = widen(narrow<CT>(rope_at(P.k_new + src, d, half, P.rope_sin + (size_t)key * half,
+                                                    P.rope_cos + (size_t)key * half)));
+        const float vin = widen(narrow<CT>(P.v_new[src + d]));
+        kl[i] = krot;
+        vl[i] = vin;
+    }
+    if (from_cache) {
+#pragma unroll
+        for (int i = 0; i < NKV; i++) {
+            const int idx = min(tid + i * NT, kExactKeys * D - 1), key = min(idx / D, nk - 1);
+            const int d = min(idx % D, Dr - 1);
+            const int kold = min(key, P.pos0 - 1);
+            const float kcache = widen(kc[(size_t)kold * P.stride_pos + d]);
+            const float vcache = widen(vc[(size_t)kold * P.stride_pos + d]);
+            if (key < P.pos0) {
+                kl[i] = kcache;
+                vl[i] = vcache;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        const int idx = tid + i * NT;
+        if (idx < kExactSlot * D) qs[idx] = (idx / D < gc && idx % D < Dr) ? qv[i] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < NKV; i++) {
+        const int idx = tid + i * NT, key = idx / D, d = idx % D;
+        if (idx < kExactKeys * D) {
+            const bool live = key < nk && d < Dr;
+            ks[key * (D + 1) + d] = live ? kl[i] : 0.0f;   // zeros: 0 * stale LDS could be NaN
+            vs[key * D + d] = live ? vl[i] : 0.0f;
+        }
+    }
+    __syncthreads();
+    // Scores, one thread per (head, key).
+    for (int t = tid; t < kExactSlot * kExactKeys; t += NT) {
+        const int h = t / kExactKeys, k = t % kExactKeys;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int d = 0; d < D; d++) acc = fmaf(qs[h * D + d], ks[k * (D + 1) + d], acc);
+        sc[t] = acc;
+    }
+    __syncthreads();
+    // Softmax over keys [0, pos], one thread per head; weights over the sum.
+    if (tid < kExactSlot) {
+        float m = -INFINITY;
+        for (int k = 0; k < nk; k++) m = fmaxf(m, sc[tid * kExactKeys + k]);
+        float l = 0.0f;
+        for (int k = 0; k < kExactKeys; k++) {
+            const float w = k < nk ? __builtin_amdgcn_exp2f(sc[tid * kExactKeys + k] - m) : 0.0f;
+            sc[tid * kExactKeys + k] = w;
+            l += w;
+        }
+        const float inv = 1.0f / l;
+        for (int k = 0; k < kExactKeys; k++) sc[tid * kExactKeys + k] *= inv;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < kExactSlot * D; idx += NT) {
+        const int h = idx / D, d = idx % D;
+        float o = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kExactKeys; k++) o = fmaf(sc[h * kExactKeys + k], vs[k * D + d], o);
+        if (h < gc && d < Dr) P.out[((size_t)r * P.H + head0 + h) * Dr + d] = o;
+    }
+}
 
 // Rows of one tile that one staging workgroup covers (two workgroups per
 // 64-key tile: 512 workgroups for a 2048-row, 8-head layer).
@@ -152,10 +314,18 @@ __global__ __launch_bounds__(kThreads) void prefill_stage(StageParams P) {
     constexpr int NIT = (NI + TPR - 1) / TPR;
     constexpr int NU = NPASS * NIT;           // (row, group) items per thread
     static_assert(RW % RPP == 0 || RPP > RW, "rows split evenly over passes");
-    __shared__ __attribute__((aligned(16))) _Float16 sv[RW][D + 4];   // 8-byte aligned rows
+    // One LDS buffer: the V rows of a staging workgroup, or an exact row's
+    // operands.
+    constexpr int kLdsFloats = ExactLds<D>::N > RW * (D + 4) / 2 ? ExactLds<D>::N : RW * (D + 4) / 2;
+    __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
+    auto sv = reinterpret_cast<_Float16 (*)[D + 4]>(lds);
 
     const int tid = threadIdx.x;
     constexpr int SPLIT = TL::KT / RW;
+    if ((int)blockIdx.y >= P.T * SPLIT) {
+        exact_row<D, CT, kThreads>(P, ((int)blockIdx.y - P.T * SPLIT) * (int)gridDim.x + (int)blockIdx.x, lds);
+        return;
+    }
     const int j = blockIdx.y / SPLIT, r0 = (blockIdx.y % SPLIT) * RW, g = blockIdx.x;
     _Float16* tk = P.tiles + ((size_t)g * P.T + j) * TL::ELEMS;
     _Float16* tv = tk + TL::K_ELEMS;
@@ -256,22 +426,6 @@ __global__ __launch_bounds__(kThreads) void prefill_stage(StageParams P) {
     }
 }
 
-// One element d of a head vector x rotated by table row (sn, cs): the two
-// fused multiply-adds of src/pickle_fast.c:1917-1922 as compiled, with the
-// pair (d, d + half) in either order; elements past 2*half are unrotated.
-__device__ __forceinline__ float rope_at(const float* x, int d, int half, const float* sn,
-                                         const float* cs) {
-    if (d < half) return fmaf(cs[d], x[d], -(sn[d] * x[d + half]));
-    if (d < 2 * half) return fmaf(sn[d - half], x[d - half], cs[d - half] * x[d]);
-    return x[d];
-}
-
-__device__ __forceinline__ float widen(float x) { return x; }
-__device__ __forceinline__ float widen(_Float16 x) { return (float)x; }
-template <typename CT> __device__ __forceinline__ CT narrow(float x);
-template <> __device__ __forceinline__ float narrow<float>(float x) { return x; }
-template <> __device__ __forceinline__ _Float16 narrow<_Float16>(float x) { return to_f16(x); }
-
 // Staging for a real head_dim Dr below the padded width D (any Dr, any
 // rotation half): one element per thread and pass, scalar loads and stores,
 // the same rotation, cache append and tile layout as prefill_stage, zeros
@@ -281,8 +435,14 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_any(StageParams P) {
     using TL = Tile<D>;
     constexpr int RW = StageRows<D>::N;
     constexpr int SPLIT = TL::KT / RW;
-    __shared__ __attribute__((aligned(16))) _Float16 sv[RW][D + 4];
+    constexpr int kLdsFloats = ExactLds<D>::N > RW * (D + 4) / 2 ? ExactLds<D>::N : RW * (D + 4) / 2;
+    __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
+    auto sv = reinterpret_cast<_Float16 (*)[D + 4]>(lds);
     const int tid = threadIdx.x;
+    if ((int)blockIdx.y >= P.T * SPLIT) {
+        exact_row<D, CT, kThreads>(P, ((int)blockIdx.y - P.T * SPLIT) * (int)gridDim.x + (int)blockIdx.x, lds);
+        return;
+    }
     const int j = blockIdx.y / SPLIT, r0 = (blockIdx.y % SPLIT) * RW, g = blockIdx.x;
     const int Dr = P.Dr;
     _Float16* tk = P.tiles + ((size_t)g * P.T + j) * TL::ELEMS;
@@ -917,7 +1077,7 @@ void prefill_attn(AttnParams P) {
                 const int cg = 32 * sub + c;
                 const int tc = qb * BM + cg / G;
                 const int d = 32 * b + 4 * u;
-                if (tc < P.n && cg % G < gc && d < Dr) {
+                if (tc < P.n && cg % G < gc && d < Dr && P.pos0 + tc >= kExactKeys) {
                     float* orow = P.out + ((size_t)tc * P.H + head0 + cg % G) * Dr;
                     if constexpr (PAD) {
                         const float ov[4] = {o.x, o.y, o.z, o.w};
@@ -933,7 +1093,7 @@ void prefill_attn(AttnParams P) {
         }
         return;
     }
-    if (!valid) return;
+    if (!valid || P.pos0 + ti < kExactKeys) return;   // rows written by the staging kernel
     float* orow = P.out + ((size_t)ti * P.H + h) * Dr;
 #pragma unroll
     for (int b = 0; b < NDB; b++) {
@@ -965,7 +1125,11 @@ int launch_dg(const PrefillArgs& a, int nsub, hipStream_t st) {
     const long long rows = (long long)a.pos0 + a.n_tokens;
     const int T = (int)((rows + TL::KT - 1) / TL::KT);
     const int HK = a.n_kv_heads;
-    if ((long long)T * (TL::KT / StageRows<D>::N) > 65535) return PKH_ERR_ARG;   // grid y limit
+    // Rows below kExactKeys: n_exact * nsub extra grid rows of HK workgroups,
+    // one per (row, head slot).
+    const int n_exact = std::max(0, std::min(a.n_tokens, kExactKeys - a.pos0));
+    if ((long long)T * (TL::KT / StageRows<D>::N) + (long long)n_exact * nsub > 65535)
+        return PKH_ERR_ARG;                                                       // grid y limit
     // A KV head's tiles are addressed with 32-bit signed byte offsets.
     if ((long long)T * TL::BYTES >= (1LL << 31)) return PKH_ERR_ARG;
     constexpr int BM = kCols / G;
@@ -994,9 +1158,15 @@ int launch_dg(const PrefillArgs& a, int nsub, hipStream_t st) {
     S.Dr = a.head_dim;
     S.T = T;
     S.tiles = static_cast<_Float16*>(tiles);
+    S.q = a.q;
+    S.out = a.out;
+    S.H = a.n_heads;
+    S.Gs = G;
+    S.nsub = nsub;
+    S.qscale = (1.0f / sqrtf((float)a.head_dim)) * 1.4426950408889634f;
     // KV head fastest: measured 9.3 against 10.0 us for the Llama-3-8B
     // 2048-row layer with the tile index fastest.
-    const dim3 sgrid(HK, T * (TL::KT / StageRows<D>::N));
+    const dim3 sgrid(HK, T * (TL::KT / StageRows<D>::N) + n_exact * nsub);
     if (pad)
         hipLaunchKernelGGL((prefill_stage_any<D, CT>), sgrid, dim3(kThreads), 0, st, S);
     else
@@ -1025,6 +1195,7 @@ int launch_dg(const PrefillArgs& a, int nsub, hipStream_t st) {
     else
         hipLaunchKernelGGL((prefill_attn<D, G, false>), agrid, ablock, 0, st, A);
     PKH_HIP(hipGetLastError());
+
     return PKH_OK;
 }
 

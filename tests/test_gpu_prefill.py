@@ -299,3 +299,30 @@ def test_prefill_graph_replay_after_tile_growth():
             big_kv.free()
         if big_rope is not None:
             big_rope.free()
+
+
+def test_prefill_error_budget_over_seeds():
+    """Twenty seeds of the Llama-3-8B-shape 2048-token prefill (H32 HK8 D128,
+    theta 5e5) against the oracle's token loop.  The worst max-abs error
+    must stay at or below 1.6e-3, 20% under the 2e-3 bound for fp16
+    operands.  Rows with at most 16 keys, where fp16 rounding costs most,
+    are computed in fp32 and must meet the fp32 tolerance, 1e-4."""
+    H, HK, D, n = 32, 8, 128, 2048
+    worst = worst_short = 0.0
+    for seed in range(100, 120):
+        ctx_k, ctx_v, q, k, v = _inputs(H, HK, D, 0, n, seed)
+        kv = DeviceKV(1, HK, D, n)
+        rope = DeviceRope(D, 5e5, n)
+        try:
+            ao = prefill_host(kv, rope, 0, 0, q, k, v)
+            ref, _, _ = _oracle_f32(ctx_k, ctx_v, 0, q, k, v, rope)
+        finally:
+            kv.free()
+            rope.free()
+        err = maxerr(ao, ref)
+        err_short = maxerr(ao[:16], ref[:16])
+        log(f"seed {seed}: max-abs err {err:.3e}, rows with <= 16 keys {err_short:.3e}")
+        worst, worst_short = max(worst, err), max(worst_short, err_short)
+    log(f"worst over 20 seeds: {worst:.3e} (rows with <= 16 keys: {worst_short:.3e})")
+    assert worst <= 1.6e-3
+    assert worst_short <= TOL_DECODE
