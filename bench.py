@@ -98,21 +98,107 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline_decode(K, V, q, k, v, cfg, layers, threads):
-    """The oracle (the reference's OpenMP-over-heads attention, restated) on
-    host copies of `layers` layers: one warm-up layer call, then one timed
-    decode step over those layers."""
+def reference_available() -> bool:
+    from oracle import pyref
+    return pyref.available()
+
+
+class _TimingModel:
+    """The compiled reference (oracle/_ref) loaded with a synthetic Llama of
+    the workload's attention shape and a hidden size of 64, so that its
+    forward pass is almost all attention; see oracle/gguf.py."""
+
+    def __init__(self, cfg, layers, ctx, tmpdir):
+        from oracle import gguf, pyref
+        self.pyref = pyref
+        path = os.path.join(tmpdir, f"timing_{cfg['H']}_{cfg['HK']}_{cfg['D']}_{layers}_{ctx}.gguf")
+        gguf.write_timing_model(path, n_layers=layers, n_heads=cfg["H"], n_kv_heads=cfg["HK"],
+                                head_dim=cfg["D"], ctx=ctx, theta=cfg["theta"])
+        self.m = pyref.RefModel(path)
+
+    def threads(self, n):
+        self.pyref.lib().ref_set_threads(n)
+
+    def fill(self, K, V, rows):
+        """Cache rows [0, rows) of every layer from host arrays [rows][HK][D]."""
+        for layer in range(self.m.n_layers):
+            self.m.kv_write(0, layer, 0, K)
+            self.m.kv_write(1, layer, 0, V)
+
+    def step(self, pos) -> float:
+        """Seconds for one token through the reference's pickle_fast_forward at
+        position pos (attending rows [0, pos])."""
+        self.m.pos = pos
+        t0 = time.perf_counter()
+        self.m.forward1(1)
+        return time.perf_counter() - t0
+
+    def prefill(self, n) -> float:
+        """Seconds for the reference's prefill of n tokens from position 0: one
+        pickle_fast_forward call, which loops over the tokens."""
+        self.m.pos = 0
+        toks = np.ones(n, np.int32)
+        logits = np.zeros(self.m.vocab_size, np.float32)
+        t0 = time.perf_counter()
+        rc = self.pyref.lib().ref_forward_n(self.m.h, toks.ctypes.data, n, logits.ctypes.data)
+        if rc != 0:
+            raise RuntimeError(f"pickle_fast_forward rc={rc}")
+        return time.perf_counter() - t0
+
+    def close(self):
+        self.m.close()
+
+
+def cpu_baseline_decode_reference(K, V, cfg, layers, threads):
+    """The reference's own attention (pickle_fast_forward of oracle/_ref, the
+    reference's sources compiled with its AVX-512 intrinsics and OpenMP over
+    heads, src/pickle_fast.c:1946-2094) at the workload's shape: one decode
+    step over `layers` layers at the workload's position, less the same
+    step at position 0 (the model's projections, RMSNorm and logits, about
+    2% of it); then one layer on one thread.  Returns seconds per
+    layer-step for `threads` threads and for one thread."""
+    import tempfile
+    ctx = cfg["ctx"]
+    kh = K[0].contiguous().cpu().numpy()[:ctx]
+    vh = V[0].contiguous().cpu().numpy()[:ctx]
+    out = {}
+    with tempfile.TemporaryDirectory() as tmp:
+        for n_layers, n_threads in ((layers, threads), (1, 1)):
+            tm = _TimingModel(cfg, n_layers, ctx + 1, tmp)
+            try:
+                tm.fill(kh, vh, ctx)
+                tm.threads(n_threads)
+                tm.step(ctx)                          # warm-up (tables, pages)
+                full = tm.step(ctx)
+                tm.step(0)
+                base = tm.step(0)
+                out[n_threads] = max(full - base, 1e-9) / n_layers
+            finally:
+                tm.close()
+    return out[threads], out[1]
+
+
+def cpu_baseline_decode_port(K, V, q, k, v, cfg, layers, threads):
+    """The oracle's restatement of the reference's OpenMP attention, built at
+    -O3 with 512-bit vectors (oracle/liboracle_avx512.so, bit-identical to
+    the -O2 oracle), on host copies of `layers` layers: one warm-up layer
+    call, then one timed decode step over those layers.  Used where the
+    compiled reference is not present."""
     from oracle import pyoracle as po
     H, HK, D, ctx = cfg["H"], cfg["HK"], cfg["D"], cfg["ctx"]
-    _, sin, cos = po.rope_tables(D, cfg["theta"], ctx + 1)
-    host = [(K[L].contiguous().cpu().numpy(), V[L].contiguous().cpu().numpy(),
-             q[L].cpu().numpy(), k[L].cpu().numpy(), v[L].cpu().numpy()) for L in range(layers)]
-    kc, vc, qq, kk, vv = host[0]
-    po.decode_step(kc, vc, ctx, qq, kk, vv, sin, cos, threads)     # warm-up
-    t0 = time.perf_counter()
-    for kc, vc, qq, kk, vv in host:
-        po.decode_step(kc, vc, ctx, qq, kk, vv, sin, cos, threads)
-    return (time.perf_counter() - t0) / layers
+    prev = po.use_build("avx512")
+    try:
+        _, sin, cos = po.rope_tables(D, cfg["theta"], ctx + 1)
+        host = [(K[L].contiguous().cpu().numpy(), V[L].contiguous().cpu().numpy(),
+                 q[L].cpu().numpy(), k[L].cpu().numpy(), v[L].cpu().numpy()) for L in range(layers)]
+        kc, vc, qq, kk, vv = host[0]
+        po.decode_step(kc, vc, ctx, qq, kk, vv, sin, cos, threads)     # warm-up
+        t0 = time.perf_counter()
+        for kc, vc, qq, kk, vv in host:
+            po.decode_step(kc, vc, ctx, qq, kk, vv, sin, cos, threads)
+        return (time.perf_counter() - t0) / layers
+    finally:
+        po.use_build(prev)
 
 
 def run_decode(args, cfg):
@@ -231,14 +317,27 @@ def run_decode(args, cfg):
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
         sample_layers = min(L, args.cpu_layers)
-        log(f"bench: CPU baseline (oracle, {threads} threads, {sample_layers} layers)")
-        t_cpu = cpu_baseline_decode(K, V, q, k, v, cfg, sample_layers, threads)
-        t_one = cpu_baseline_decode(K, V, q, k, v, cfg, 1, 1)
+        if reference_available():
+            log(f"bench: CPU baseline (the compiled reference, {threads} threads, "
+                f"{sample_layers} layers; then 1 thread, 1 layer)")
+            t_cpu, t_one = cpu_baseline_decode_reference(K, V, cfg, sample_layers, threads)
+            kind, build = "reference", ("the reference's src/pickle_fast.c compiled from its own "
+                                        "sources (oracle/Makefile: -O3 -march=x86-64-v4 -fopenmp, "
+                                        "its AVX-512 score and PV loops)")
+            sample = (f"pickle_fast_forward of that build, one decode step over {sample_layers} "
+                      f"layer(s) at position {ctx} of a synthetic Llama with this attention shape "
+                      f"and hidden size 64 (oracle/gguf.py), cache rows N(0,1), less the same "
+                      f"step at position 0 (its projections, ~2%)")
+        else:
+            log(f"bench: CPU baseline (oracle AVX-512 build, {threads} threads, {sample_layers} layers)")
+            t_cpu = cpu_baseline_decode_port(K, V, q, k, v, cfg, sample_layers, threads)
+            t_one = cpu_baseline_decode_port(K, V, q, k, v, cfg, 1, 1)
+            kind, build = "port", ("oracle/pk_oracle.c at -O3 -march=x86-64-v4 "
+                                   "-mprefer-vector-width=512, bit-identical to the -O2 oracle")
+            sample = (f"one decode step over {sample_layers} layer(s) of the same workload "
+                      f"({ctx} cached rows each)")
         cpu = {"value": round(bpl / t_cpu / 1e9, 3), "unit": "GB/s", "cores": threads,
-               "kind": "port",
-               "sample": (f"one decode step over {sample_layers} layer(s) of the same workload "
-                          f"({ctx} cached rows each) with the oracle's restatement of the "
-                          f"reference's OpenMP-over-heads attention (oracle/pk_oracle.c)"),
+               "kind": kind, "build": build, "sample": sample,
                "us_per_layer_step": round(t_cpu * 1e6, 2),
                "cpu_model": cpu_model(),
                "one_thread": {"value": round(bpl / t_one / 1e9, 3), "unit": "GB/s",
@@ -283,9 +382,9 @@ def prefill_flops(H: int, D: int, S: int, pos0: int = 0) -> int:
     return 4 * D * H * pairs
 
 
-def cpu_baseline_prefill(q, k, v, cfg, threads):
-    """The oracle's token loop (the reference's prefill: one decode step per
-    prompt token) on one layer of the workload."""
+def oracle_prefill(q, k, v, cfg, threads):
+    """The oracle's token loop (one restated decode step per prompt token) on
+    one layer of the workload: the parity reference for the GPU outputs."""
     from oracle import pyoracle as po
     H, HK, D, S = cfg["H"], cfg["HK"], cfg["D"], cfg["S"]
     _, sin, cos = po.rope_tables(D, cfg["theta"], S)
@@ -295,6 +394,27 @@ def cpu_baseline_prefill(q, k, v, cfg, threads):
     t0 = time.perf_counter()
     ao = po.prefill(kc, vc, 0, qq, kk, vv, sin, cos, threads)
     return time.perf_counter() - t0, ao
+
+
+def cpu_baseline_prefill_reference(cfg, threads):
+    """The reference's prefill (pickle_fast_forward over the prompt: one
+    decode step per token through every layer, src/pickle_fast.c:1881-1898)
+    of oracle/_ref on a one-layer synthetic model of the workload's attention
+    shape, less that model's per-token cost outside attention (the same
+    forward at position 0, times the prompt length).  Seconds per layer."""
+    import tempfile
+    S = cfg["S"]
+    with tempfile.TemporaryDirectory() as tmp:
+        tm = _TimingModel(cfg, 1, S, tmp)
+        try:
+            tm.threads(threads)
+            tm.prefill(min(S, 64))                   # warm-up
+            total = tm.prefill(S)
+            tm.step(0)
+            base = min(tm.step(0) for _ in range(5))
+        finally:
+            tm.close()
+    return max(total - S * base, 1e-9), total
 
 
 def run_prefill(args, cfg, name):
@@ -373,16 +493,37 @@ def run_prefill(args, cfg, name):
     errs = []
     threads = min(16, os.cpu_count() or 1)
     if not args.no_cpu_baseline:
-        log(f"bench: CPU baseline (oracle token loop, {threads} threads, 1 layer)")
-        t_cpu, ref0 = cpu_baseline_prefill(q[0], k[0], v[0], cfg, threads)
-        errs.append(float(np.max(np.abs(ao[0].cpu().numpy() - ref0))))
-        cpu = {"value": round(fl / t_cpu / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-               "kind": "port",
-               "sample": (f"one layer's {S}-token causal prefill of the same workload with the "
-                          f"oracle's token loop (one restated reference decode step per "
-                          f"token, oracle/pk_oracle.c)"),
-               "us_per_layer": round(t_cpu * 1e6, 1)}
-    for layer in sorted({L - 1} | (set() if errs else {0})):
+        if reference_available():
+            log(f"bench: CPU baseline (the compiled reference's token loop, {threads} threads, 1 layer)")
+            t_cpu, t_total = cpu_baseline_prefill_reference(cfg, threads)
+            cpu = {"value": round(fl / t_cpu / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+                   "kind": "reference",
+                   "build": ("the reference's src/pickle_fast.c compiled from its own sources "
+                             "(oracle/Makefile: -O3 -march=x86-64-v4 -fopenmp)"),
+                   "sample": (f"pickle_fast_forward of that build over a {S}-token prompt from "
+                              f"position 0 (its token loop) on a one-layer synthetic Llama with "
+                              f"this attention shape and hidden size 64, less {S} times the "
+                              f"model's one-token cost at position 0 (its projections)"),
+                   "us_per_layer": round(t_cpu * 1e6, 1),
+                   "us_per_layer_with_projections": round(t_total * 1e6, 1),
+                   "cpu_model": cpu_model()}
+        else:
+            log(f"bench: CPU baseline (oracle token loop, AVX-512 build, {threads} threads, 1 layer)")
+            from oracle import pyoracle as po
+            prev = po.use_build("avx512")
+            try:
+                t_cpu, _ = oracle_prefill(q[0], k[0], v[0], cfg, threads)
+            finally:
+                po.use_build(prev)
+            cpu = {"value": round(fl / t_cpu / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+                   "kind": "port",
+                   "build": ("oracle/pk_oracle.c at -O3 -march=x86-64-v4 "
+                             "-mprefer-vector-width=512, bit-identical to the -O2 oracle"),
+                   "sample": (f"one layer's {S}-token causal prefill of the same workload with "
+                              f"the oracle's token loop (one restated reference decode step "
+                              f"per token)"),
+                   "us_per_layer": round(t_cpu * 1e6, 1)}
+    for layer in sorted({0, L - 1}):
         _, osin, ocos = po.rope_tables(D, cfg["theta"], S)
         kc = np.zeros((S, HK, D), np.float32)
         vc = np.zeros_like(kc)
@@ -535,17 +676,26 @@ def run_ragged(args, cfg, name):
     achieved = bpl / avg_launch / 1e9
 
     threads = min(16, os.cpu_count() or 1)
-    log(f"bench: ragged parity + CPU baseline (oracle, {threads} threads, layer 0)")
-    t_cpu, ref = cpu_baseline_ragged(KV, ctx, slot0, q, k, v, cfg, threads)
+    log(f"bench: ragged parity + CPU baseline (oracle AVX-512 build, {threads} threads, layer 0)")
+    from oracle import pyoracle as po
+    prev = po.use_build("avx512")
+    try:
+        t_cpu, ref = cpu_baseline_ragged(KV, ctx, slot0, q, k, v, cfg, threads)
+    finally:
+        po.use_build(prev)
     err = float(np.max(np.abs(ao[0].cpu().numpy() - ref)))
     log(f"bench: ragged max-abs err vs oracle: {err:.3e}")
     cpu = None
     if not args.no_cpu_baseline:
         cpu = {"value": round(bpl / t_cpu / 1e9, 3), "unit": "GB/s", "cores": threads,
                "kind": "port",
+               "build": ("oracle/pk_oracle.c at -O3 -march=x86-64-v4 -mprefer-vector-width=512, "
+                         "bit-identical to the -O2 oracle (the reference has no fp16 cache and "
+                         "no batch API, so there is no reference build to time)"),
                "sample": (f"one layer of the same step: the oracle's fp16-KV decode step "
-                          f"looped over the {n} sequences (oracle/pk_oracle.c)"),
-               "us_per_layer_step": round(t_cpu * 1e6, 1)}
+                          f"looped over the {n} sequences"),
+               "us_per_layer_step": round(t_cpu * 1e6, 1),
+               "cpu_model": cpu_model()}
     lib.pkh_plan_free(plan)
     lib.pkh_rope_free(rp)
     return {

@@ -159,3 +159,35 @@ def write_probe(path: str, *, n_heads, n_kv_heads, head_dim, theta, ctx, seed, v
     meta = llama_meta(n_layers=1, hidden=hd, ffn=ff, n_heads=H, n_kv_heads=HK, head_dim=D,
                       ctx=ctx, vocab=vocab, theta=theta, name="attention-probe")
     write_gguf(path, meta, t)
+
+
+# ---- timing model for the CPU baseline --------------------------------------
+
+def write_timing_model(path: str, *, n_layers, n_heads, n_kv_heads, head_dim, ctx, theta,
+                       hidden=64, ffn=64, vocab=256, seed=0):
+    """A Llama model with the attention shape (H, HK, head_dim) of a real
+    model and a small hidden size, so that the reference's forward pass at a
+    long context is almost all attention (src/pickle_fast.c:1946-2094): its
+    Q/K/V/O projections are H*head_dim x hidden (src/pickle_fast.c:1903-1908,
+    2112), and head_dim comes from llama.rope.dimension_count
+    (src/pickle.c:1006-1007).  Weights N(0, 0.02), F32."""
+    H, HK, D = n_heads, n_kv_heads, head_dim
+    rng = np.random.default_rng(seed)
+    w = lambda *shape: (rng.standard_normal(shape) * 0.02).astype(np.float32)
+    t = [("token_embd.weight", w(vocab, hidden))]
+    for L in range(n_layers):
+        t += [
+            (f"blk.{L}.attn_norm.weight", np.ones(hidden, np.float32)),
+            (f"blk.{L}.attn_q.weight", w(H * D, hidden)),
+            (f"blk.{L}.attn_k.weight", w(HK * D, hidden)),
+            (f"blk.{L}.attn_v.weight", w(HK * D, hidden)),
+            (f"blk.{L}.attn_output.weight", w(hidden, H * D)),
+            (f"blk.{L}.ffn_norm.weight", np.ones(hidden, np.float32)),
+            (f"blk.{L}.ffn_gate.weight", w(ffn, hidden)),
+            (f"blk.{L}.ffn_up.weight", w(ffn, hidden)),
+            (f"blk.{L}.ffn_down.weight", w(hidden, ffn)),
+        ]
+    t += [("output_norm.weight", np.ones(hidden, np.float32)), ("output.weight", w(vocab, hidden))]
+    meta = llama_meta(n_layers=n_layers, hidden=hidden, ffn=ffn, n_heads=H, n_kv_heads=HK,
+                      head_dim=D, ctx=ctx, vocab=vocab, theta=theta, name="attention-timing")
+    write_gguf(path, meta, t)

@@ -16,21 +16,36 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
+# The same source at -O3 with 512-bit vectors: bit-identical results (checked
+# in tests/test_oracle.py), used to time the CPU baseline.
+LIB_AVX512_PATH = os.path.join(HERE, "liboracle_avx512.so")
+BUILDS = {"plain": LIB_PATH, "avx512": LIB_AVX512_PATH}
 REF_LIB_PATH = os.path.join(HERE, "_ref", "libpickle_ref.so")
 
-_lib = None
+_libs: dict = {}
+_build = "plain"
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
 _Z = ctypes.c_size_t
 
 
+def use_build(name: str) -> str:
+    """Select the oracle build the wrappers below call ("plain", the -O2
+    build, or "avx512"); returns the previous selection."""
+    global _build
+    if name not in BUILDS:
+        raise ValueError(name)
+    prev, _build = _build, name
+    return prev
+
+
 def lib() -> ctypes.CDLL:
-    global _lib
-    if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise FileNotFoundError(f"{LIB_PATH} missing: run `make -C oracle`")
-        L = ctypes.CDLL(LIB_PATH)
+    if _build not in _libs:
+        path = BUILDS[_build]
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        L = ctypes.CDLL(path)
         sig = {
             "pko_rope_half": (_I, [_I]),
             "pko_rope_inv_freq": (None, [_P, _I, _F]),
@@ -54,8 +69,8 @@ def lib() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
-        _lib = L
-    return _lib
+        _libs[_build] = L
+    return _libs[_build]
 
 
 def _ptr(a: np.ndarray) -> int:

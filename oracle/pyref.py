@@ -48,6 +48,8 @@ def lib() -> ctypes.CDLL:
             "ref_rope": (_I, [_P, _I, _Z, _Z, _P]),
             "ref_argmax": (ctypes.c_int32, [_P, _Z]),
             "ref_selftest": (_I, [ctypes.POINTER(ctypes.c_int32)]),
+            "ref_set_threads": (None, [_I]),
+            "ref_get_threads": (_I, []),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)

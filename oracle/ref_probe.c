@@ -16,6 +16,7 @@
  *     buffers (xn, q, k, v, ao: src/pickle_fast.h:105-110), which hold the
  *     last layer's values after a forward call.
  */
+#include <omp.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -154,6 +155,11 @@ int ref_rope(void* p, int which, size_t p0, size_t n, float* dst) {
     memcpy(dst, src, n * (size_t)half * sizeof(float));
     return PICKLE_OK;
 }
+
+/* OpenMP threads of the reference's parallel loops (its attention runs
+ * `omp parallel for` over heads, src/pickle_fast.c:1960). */
+void ref_set_threads(int n) { omp_set_num_threads(n); }
+int  ref_get_threads(void) { return omp_get_max_threads(); }
 
 int32_t ref_argmax(const float* logits, size_t n) {
     return pickle_fast_argmax(logits, n);

@@ -37,7 +37,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, HERE)
 
-import gguf  # noqa: E402
+from oracle import gguf  # noqa: E402
 from oracle import pyref  # noqa: E402
 
 # name: (H, HK, D, theta, pos, seed)

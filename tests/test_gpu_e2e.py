@@ -26,7 +26,7 @@ from pkh_util import DeviceKV, DeviceRope, decode_host, log, maxerr, prefill_hos
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "golden"))
-import gguf  # noqa: E402
+from oracle import gguf  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 

@@ -14,6 +14,7 @@ import glob
 import hashlib
 import json
 import os
+import re
 
 import numpy as np
 import pytest
@@ -249,7 +250,7 @@ def test_reference_selftest_still_passes():
 @pytest.mark.parametrize("H,HK,D,theta,pos", [(8, 2, 64, 1e4, 700), (4, 2, 128, 5e5, 1500),
                                                (4, 4, 16, 1e4, 3)])
 def test_oracle_matches_live_reference(tmp_path, H, HK, D, theta, pos):
-    import gguf
+    from oracle import gguf
     path = str(tmp_path / "probe.gguf")
     gguf.write_probe(path, n_heads=H, n_kv_heads=HK, head_dim=D, theta=theta, ctx=pos + 4,
                      seed=pos)
@@ -282,7 +283,7 @@ def test_oracle_matches_live_reference(tmp_path, H, HK, D, theta, pos):
 def test_reference_range_errors(tmp_path):
     """pos >= max_seq and token >= vocab are PICKLE_ERR_RANGE in the reference
     (src/pickle_fast.c:1883-1885); the GPU entry points keep the pos check."""
-    import gguf
+    from oracle import gguf
     path = str(tmp_path / "probe.gguf")
     gguf.write_probe(path, n_heads=2, n_kv_heads=1, head_dim=16, theta=1e4, ctx=4, seed=0)
     with pyref.RefModel(path) as m:
@@ -290,3 +291,78 @@ def test_reference_range_errors(tmp_path):
         assert m.forward1_rc(1) == -7
         m.pos = 0
         assert m.forward1_rc(8) == -7
+
+
+def _run_all_builds(fn):
+    """fn() under each oracle build; returns the results by build."""
+    out = {}
+    for build in ("plain", "avx512"):
+        prev = po.use_build(build)
+        try:
+            out[build] = fn()
+        finally:
+            po.use_build(prev)
+    return out
+
+
+@pytest.mark.parametrize("path", PROBES, ids=[os.path.basename(p)[11:-4] for p in PROBES])
+def test_avx512_build_is_bit_identical_on_probes(path):
+    """The CPU baseline's build of the oracle (-O3, 512-bit vectors) gives the
+    -O2 build's results bit for bit on the reference's golden probes."""
+    z = np.load(path)
+    H, HK, D, pos, theta, sin, cos, kc, vc = _probe_inputs(z)
+
+    def run():
+        return po.decode_step(kc.copy(), vc.copy(), pos, z["q"], z["k"], z["v"], sin, cos, 4)[0]
+
+    r = _run_all_builds(run)
+    assert np.array_equal(r["plain"], r["avx512"])
+    assert np.abs(r["avx512"] - z["ao"]).max() <= 1e-6
+
+
+@pytest.mark.parametrize("H,HK,D,pos", [(32, 8, 128, 3000), (8, 2, 24, 500), (6, 4, 16, 300),
+                                        (4, 2, 80, 900), (7, 3, 96, 257)])
+def test_avx512_build_is_bit_identical_on_random_steps(H, HK, D, pos):
+    """Decode (fp32 and fp16 caches) and a short prefill, on random inputs
+    with the scalar (head_dim % 16 != 0) and 16-lane score loops."""
+    rng = np.random.default_rng(H * 1000 + D + pos)
+    kc0 = rng.standard_normal((pos + 1, HK, D), dtype=np.float32)
+    vc0 = rng.standard_normal((pos + 1, HK, D), dtype=np.float32)
+    q = rng.standard_normal((H, D), dtype=np.float32)
+    k = rng.standard_normal((HK, D), dtype=np.float32)
+    v = rng.standard_normal((HK, D), dtype=np.float32)
+    qn = rng.standard_normal((9, H, D), dtype=np.float32)
+    kn = rng.standard_normal((9, HK, D), dtype=np.float32)
+    vn = rng.standard_normal((9, HK, D), dtype=np.float32)
+    _, sin, cos = po.rope_tables(D, 5e5, pos + 10)
+
+    def run():
+        a = po.decode_step(kc0.copy(), vc0.copy(), pos, q, k, v, sin, cos, 4)[0]
+        b = po.decode_step_f16(po.f32_to_f16_bits(kc0), po.f32_to_f16_bits(vc0), pos, q, k, v,
+                               sin, cos, 4)
+        kc = np.zeros((pos + 10, HK, D), np.float32)
+        vc = np.zeros_like(kc)
+        kc[:pos + 1], vc[:pos + 1] = kc0, vc0
+        c = po.prefill(kc, vc, pos + 1, qn, kn, vn, sin, cos, 4)
+        return a, b, c
+
+    r = _run_all_builds(run)
+    for x, y in zip(r["plain"], r["avx512"]):
+        assert np.array_equal(x, y)
+
+
+def test_avx512_build_uses_512_bit_fma():
+    """The CPU baseline's build really is vectorised: its code holds 512-bit
+    fused multiply-adds, the -O2 build's none."""
+    import shutil
+    import subprocess
+    objdump = shutil.which("objdump")
+    if not objdump:
+        pytest.skip("no objdump")
+
+    def zmm_fmas(path):
+        text = subprocess.run([objdump, "-d", path], capture_output=True, text=True, check=True).stdout
+        return len(re.findall(r"vfmadd\w+ps\s+%zmm", text))
+
+    assert zmm_fmas(po.LIB_AVX512_PATH) > 0
+    assert zmm_fmas(po.LIB_PATH) == 0
