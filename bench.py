@@ -302,6 +302,26 @@ def run_decode(args, cfg):
     avg_launch = float(durs.mean())
     achieved = bpl / avg_launch / 1e9
 
+    # The host-pointer entry the seam binding uses (pkh_attn_decode with q, k,
+    # v and ao in pageable host memory, as the reference's state buffers
+    # are): one packed upload, the kernel, one download per layer call.  PCIe
+    # included; reported beside the device-resident figure, never in value.
+    hq = [np.ascontiguousarray(q[i].cpu().numpy()) for i in range(L)]
+    hk = [np.ascontiguousarray(k[i].cpu().numpy()) for i in range(L)]
+    hv = [np.ascontiguousarray(v[i].cpu().numpy()) for i in range(L)]
+    hao = np.zeros((H, D), np.float32)
+    host_steps = max(2, args.steps // 4)
+    for layer in range(L):
+        pk.check(lib.pkh_attn_decode(kvp, rp, layer, ctx, H, hq[layer].ctypes.data, hk[layer].ctypes.data,
+                                     hv[layer].ctypes.data, hao.ctypes.data), "pkh_attn_decode")
+    t0 = time.perf_counter()
+    for _ in range(host_steps):
+        for layer in range(L):
+            lib.pkh_attn_decode(kvp, rp, layer, ctx, H, hq[layer].ctypes.data, hk[layer].ctypes.data,
+                                hv[layer].ctypes.data, hao.ctypes.data)
+    host_us = (time.perf_counter() - t0) / (host_steps * L) * 1e6
+    log(f"bench: host-pointer entry {host_us:.2f} us/layer-step (PCIe both ways included)")
+
     # Parity of the benchmarked outputs (first and last layer) against the oracle.
     _, osin, ocos = po.rope_tables(D, cfg["theta"], max_seq)
     errs = []
@@ -363,6 +383,7 @@ def run_decode(args, cfg):
                    "rope_theta": cfg["theta"], "new_token_pos": ctx},
         "us_per_layer_step": round(wall / n_launch * 1e6, 3),
         "eager_us_per_layer_step": round(eager_wall / n_launch * 1e6, 3),
+        "host_entry_us_per_layer_step": round(host_us, 2),
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "bytes_per_layer_step": bpl,
         "max_abs_err_vs_oracle": max(errs),

@@ -24,6 +24,7 @@ Buf g_scratch[kMaxDevices];
 Buf g_staging[kMaxDevices][4];
 Buf g_tiles[kMaxDevices];
 Buf g_counters[kMaxDevices];
+Buf g_pinned[kMaxDevices];        // pinned host staging of the host-pointer entry points
 
 // Buffers outgrown by a larger call.  They are never freed: a HIP graph
 // captured earlier holds their addresses and may still be replayed.  Growth
@@ -93,6 +94,53 @@ int staging_get(int slot, size_t bytes, void** out) {
 }
 
 int tiles_get(size_t bytes, void** out) { return grow(g_tiles[g_device], bytes, out); }
+
+// Pinned host staging for the host-pointer entry points.  Nothing captured
+// refers to it (those entry points synchronize), so an outgrown buffer is
+// freed.
+int pinned_get(size_t bytes, void** out) {
+    Buf& b = g_pinned[g_device];
+    if (bytes <= b.bytes && b.ptr) {
+        *out = b.ptr;
+        return PKH_OK;
+    }
+    size_t want = bytes < 65536 ? 65536 : bytes;
+    if (b.ptr && want < 2 * b.bytes) want = 2 * b.bytes;
+    void* p = nullptr;
+    PKH_HIP(hipHostMalloc(&p, want, hipHostMallocDefault));
+    if (b.ptr) (void)hipHostFree(b.ptr);
+    b.ptr = p;
+    b.bytes = want;
+    *out = p;
+    return PKH_OK;
+}
+
+// Host-pointer calls: q, k, v (and ao) in one pinned block and one device
+// block, each segment 256-byte aligned, so a call costs one upload and one
+// download.
+struct HostStage {
+    char* host = nullptr;
+    char* dev = nullptr;
+    size_t off_k = 0, off_v = 0, off_ao = 0, in_bytes = 0, out_bytes = 0;
+};
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+int host_stage(size_t q_bytes, size_t kv_bytes, size_t ao_bytes, HostStage* hs) {
+    hs->off_k = align256(q_bytes);
+    hs->off_v = hs->off_k + align256(kv_bytes);
+    hs->in_bytes = hs->off_v + kv_bytes;
+    hs->off_ao = align256(hs->in_bytes);
+    hs->out_bytes = ao_bytes;
+    void *h = nullptr, *d = nullptr;
+    int rc = pinned_get(hs->off_ao + ao_bytes, &h);
+    if (rc != PKH_OK) return rc;
+    rc = staging_get(0, hs->off_ao + ao_bytes, &d);
+    if (rc != PKH_OK) return rc;
+    hs->host = static_cast<char*>(h);
+    hs->dev = static_cast<char*>(d);
+    return PKH_OK;
+}
 
 }  // namespace pkh
 
@@ -264,6 +312,31 @@ extern "C" int pkh_rope_upload(pkh_rope_t* rope, const float* sin_tab, const flo
 
 namespace {
 
+// The host-pointer entry points' transfers around `launch` (which enqueues
+// on the null stream): q, k and v copied into the pinned block and sent in
+// one upload, ao returned in one download.
+template <typename Launch>
+int host_call(size_t q_bytes, size_t kv_bytes, const float* q, const float* k, const float* v,
+              float* ao, Launch launch) {
+    HostStage hs;
+    int rc = host_stage(q_bytes, kv_bytes, q_bytes, &hs);
+    if (rc != PKH_OK) return rc;
+    std::memcpy(hs.host, q, q_bytes);
+    std::memcpy(hs.host + hs.off_k, k, kv_bytes);
+    std::memcpy(hs.host + hs.off_v, v, kv_bytes);
+    PKH_HIP(hipMemcpyAsync(hs.dev, hs.host, hs.in_bytes, hipMemcpyHostToDevice, nullptr));
+    rc = launch(hs.dev, hs);
+    if (rc != PKH_OK) {
+        (void)hipStreamSynchronize(nullptr);   // the upload still reads the pinned block
+        return rc;
+    }
+    PKH_HIP(hipMemcpyAsync(hs.host + hs.off_ao, hs.dev + hs.off_ao, hs.out_bytes,
+                           hipMemcpyDeviceToHost, nullptr));
+    PKH_HIP(hipStreamSynchronize(nullptr));
+    std::memcpy(ao, hs.host + hs.off_ao, hs.out_bytes);
+    return PKH_OK;
+}
+
 int check_common(int head_dim, int n_heads, int n_kv_heads, const pkh_rope_t* rope) {
     if (!shape_supported(head_dim, n_heads, n_kv_heads)) return PKH_ERR_ARG;
     if (!rope || !rope->sin || !rope->cos) return PKH_ERR_ARG;
@@ -347,21 +420,13 @@ extern "C" int pkh_attn_decode(const pkh_kv_t* kv, const pkh_rope_t* rope, int l
     int rc = decode_validate(kv, rope, layer, pos, n_heads);
     if (rc != PKH_OK) return rc;
     if (!q || !k || !v || !ao) return PKH_ERR_ARG;
-    const size_t qn = (size_t)n_heads * kv->head_dim;
-    const size_t kn = (size_t)kv->n_kv_heads * kv->head_dim;
-    void *dq, *dk, *dv, *dao;
-    if ((rc = staging_get(0, qn * sizeof(float), &dq)) != PKH_OK) return rc;
-    if ((rc = staging_get(1, kn * sizeof(float), &dk)) != PKH_OK) return rc;
-    if ((rc = staging_get(2, kn * sizeof(float), &dv)) != PKH_OK) return rc;
-    if ((rc = staging_get(3, qn * sizeof(float), &dao)) != PKH_OK) return rc;
-    PKH_HIP(hipMemcpy(dq, q, qn * sizeof(float), hipMemcpyHostToDevice));
-    PKH_HIP(hipMemcpy(dk, k, kn * sizeof(float), hipMemcpyHostToDevice));
-    PKH_HIP(hipMemcpy(dv, v, kn * sizeof(float), hipMemcpyHostToDevice));
-    rc = decode_checked(kv, rope, layer, pos, n_heads, (const float*)dq, (const float*)dk,
-                        (const float*)dv, (float*)dao, nullptr);
-    if (rc != PKH_OK) return rc;
-    PKH_HIP(hipMemcpy(ao, dao, qn * sizeof(float), hipMemcpyDeviceToHost));
-    return PKH_OK;
+    const size_t qb = (size_t)n_heads * kv->head_dim * sizeof(float);
+    const size_t kb = (size_t)kv->n_kv_heads * kv->head_dim * sizeof(float);
+    return host_call(qb, kb, q, k, v, ao, [&](const char* d, const HostStage& hs) {
+        return decode_checked(kv, rope, layer, pos, n_heads, (const float*)d,
+                              (const float*)(d + hs.off_k), (const float*)(d + hs.off_v),
+                              (float*)(d + hs.off_ao), nullptr);
+    });
 }
 
 // ---------------------------------------------------------------------------
@@ -428,21 +493,13 @@ extern "C" int pkh_attn_prefill(const pkh_kv_t* kv, const pkh_rope_t* rope, int 
     int rc = prefill_validate(kv, rope, layer, pos0, n_tokens, n_heads);
     if (rc != PKH_OK) return rc;
     if (!q || !k || !v || !ao) return PKH_ERR_ARG;
-    const size_t qn = (size_t)n_tokens * n_heads * kv->head_dim;
-    const size_t kn = (size_t)n_tokens * kv->n_kv_heads * kv->head_dim;
-    void *dq, *dk, *dv, *dao;
-    if ((rc = staging_get(0, qn * sizeof(float), &dq)) != PKH_OK) return rc;
-    if ((rc = staging_get(1, kn * sizeof(float), &dk)) != PKH_OK) return rc;
-    if ((rc = staging_get(2, kn * sizeof(float), &dv)) != PKH_OK) return rc;
-    if ((rc = staging_get(3, qn * sizeof(float), &dao)) != PKH_OK) return rc;
-    PKH_HIP(hipMemcpy(dq, q, qn * sizeof(float), hipMemcpyHostToDevice));
-    PKH_HIP(hipMemcpy(dk, k, kn * sizeof(float), hipMemcpyHostToDevice));
-    PKH_HIP(hipMemcpy(dv, v, kn * sizeof(float), hipMemcpyHostToDevice));
-    rc = prefill_checked(kv, rope, layer, pos0, n_tokens, n_heads, (const float*)dq,
-                         (const float*)dk, (const float*)dv, (float*)dao, nullptr);
-    if (rc != PKH_OK) return rc;
-    PKH_HIP(hipMemcpy(ao, dao, qn * sizeof(float), hipMemcpyDeviceToHost));
-    return PKH_OK;
+    const size_t qb = (size_t)n_tokens * n_heads * kv->head_dim * sizeof(float);
+    const size_t kb = (size_t)n_tokens * kv->n_kv_heads * kv->head_dim * sizeof(float);
+    return host_call(qb, kb, q, k, v, ao, [&](const char* d, const HostStage& hs) {
+        return prefill_checked(kv, rope, layer, pos0, n_tokens, n_heads, (const float*)d,
+                               (const float*)(d + hs.off_k), (const float*)(d + hs.off_v),
+                               (float*)(d + hs.off_ao), nullptr);
+    });
 }
 
 // ---------------------------------------------------------------------------

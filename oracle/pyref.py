@@ -49,6 +49,9 @@ def lib() -> ctypes.CDLL:
             "ref_argmax": (ctypes.c_int32, [_P, _Z]),
             "ref_selftest": (_I, [ctypes.POINTER(ctypes.c_int32)]),
             "ref_set_threads": (None, [_I]),
+            "ref_state_ptr": (_P, [_P]),
+            "ref_arch_ptr": (_P, [_P]),
+            "ref_write_state": (_I, [_P, _I, _P, _Z]),
             "ref_get_threads": (_I, []),
         }
         for name, (res, args) in sig.items():

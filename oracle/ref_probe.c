@@ -105,6 +105,25 @@ int ref_forward_stateless(void* p, int32_t token, float* logits) {
                                logits, NULL, NULL);
 }
 
+/* The handle's fast state and arch, for code that takes the reference's own
+ * structs (the seam binding's tests). */
+void* ref_state_ptr(void* p) { return &((ref_handle_t*)p)->state; }
+void* ref_arch_ptr(void* p) { return &((ref_handle_t*)p)->arch; }
+
+/* which: 1 q, 2 k, 3 v.  Copies n floats into the state's work buffer. */
+int ref_write_state(void* p, int which, const float* src, size_t n) {
+    ref_handle_t* h = (ref_handle_t*)p;
+    float* dst = NULL;
+    switch (which) {
+        case 1: dst = h->state.q; break;
+        case 2: dst = h->state.k; break;
+        case 3: dst = h->state.v; break;
+        default: return PICKLE_ERR_ARG;
+    }
+    memcpy(dst, src, n * sizeof(float));
+    return PICKLE_OK;
+}
+
 /* which: 0 xn, 1 q, 2 k, 3 v, 4 ao.  Copies n floats out. */
 int ref_read_state(void* p, int which, float* dst, size_t n) {
     ref_handle_t* h = (ref_handle_t*)p;

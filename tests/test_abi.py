@@ -181,3 +181,28 @@ def test_header_builds_and_links_from_c99(tmp_path):
     r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
     assert "c host ok" in r.stdout
+
+
+def test_seam_binding_compiles_against_the_reference_headers(tmp_path):
+    """lestramanika_amd/host/pickle_seam.c -- the binding a pickle maintainer
+    adds -- compiles as C11 with warnings as errors against the reference's
+    own src/pickle.h and src/pickle_fast.h (its static asserts check that
+    pkh_kv_t mirrors pickle_fast_kv_t field by field and that the status
+    codes agree), and links against libpkh.so and the compiled reference
+    with no undefined symbol.  Needs the reference tree, which only this
+    build container has."""
+    import shutil
+    import subprocess
+    from oracle import pyref
+    src = "/root/reference/src"
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if not cc or not os.path.isdir(src) or not pyref.available():
+        pytest.skip("reference tree or compiled reference not present")
+    out = tmp_path / "libseam.so"
+    cmd = [cc, "-std=c11", "-O2", "-Wall", "-Wextra", "-Werror", "-fPIC", "-shared",
+           "-Wl,--no-undefined", f"-I{src}", f"-I{os.path.join(ROOT, 'include')}",
+           "-o", str(out), os.path.join(ROOT, "lestramanika_amd", "host", "pickle_seam.c"),
+           f"-L{os.path.join(ROOT, 'lestramanika_amd')}", "-lpkh",
+           f"-L{os.path.dirname(pyref.REF_LIB_PATH)}", "-lpickle_ref"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
