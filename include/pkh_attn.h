@@ -269,13 +269,31 @@ int  pkh_kv_batch_alloc(int n_layers, int n_kv_heads, int head_dim,
 void pkh_kv_batch_free(pkh_kv_batch_t* kvb);
 
 /* A decode plan: the positions of the next token of every sequence and the
- * split of each sequence's context into work items.  Build it once per step
- * (positions change every step); it is reused by every layer of the step. */
+ * split of each sequence's context into work items of a fixed size (chosen
+ * from the positions given to pkh_plan_create).  The plan's grid covers each
+ * sequence's whole capacity (max_seq[s]), so the same plan -- and a HIP
+ * graph captured around the decode calls that use it -- serves every later
+ * step: move the positions with pkh_plan_update, which allocates nothing and
+ * does not synchronize the device.  pkh_plan_create allocates and copies
+ * synchronously; call it once, outside any capture. */
 typedef struct pkh_plan pkh_plan_t;
 
 int  pkh_plan_create(const pkh_kv_batch_t* kvb, const int* pos, int n_heads,
                      pkh_plan_t** plan);
 void pkh_plan_free(pkh_plan_t* plan);
+
+/* The positions of the next step, pos[s] for each sequence, written into the
+ * plan's device copy on `stream` (hipMemcpyAsync; no allocation, no device
+ * synchronization).  pos[s] outside [0, max_seq[s]) returns PKH_ERR_RANGE
+ * and enqueues nothing.  The copy reads pos when the stream reaches it:
+ * pageable memory is read before the call returns; pinned memory is read
+ * later, so keep it unchanged until then.  Under stream capture the copy is
+ * recorded as a graph node that reads pinned pos on every replay: changing
+ * that pinned array between replays advances a captured step (the host
+ * cannot check replayed positions; a position past a sequence's capacity
+ * gives NaN for that sequence and writes no cache row).  No counterpart in
+ * the reference (docs/ROADMAP.md:56-58 plans continuous batching). */
+int  pkh_plan_update(pkh_plan_t* plan, const int* pos, void* stream);
 
 /* One decode step of every sequence on one layer: q [n_seqs][H][D],
  * k/v [n_seqs][HK][D], ao [n_seqs][H][D], device pointers. */
@@ -283,6 +301,17 @@ int pkh_attn_decode_batch_async(const pkh_kv_batch_t* kvb,
                                 const pkh_rope_t* rope, const pkh_plan_t* plan,
                                 int layer, const float* d_q, const float* d_k,
                                 const float* d_v, float* d_ao, void* stream);
+
+/* Causal prefill of n_tokens tokens of sequence `seq` into its slots of a
+ * batch cache, as pkh_attn_prefill_async does for a single cache (the token
+ * loop of src/pickle_fast.c:1881-1898 for one sequence): rows pos0 + i of
+ * sequence seq receive the rotated k and v, and each token attends that
+ * sequence's rows [0, pos0 + i].  Device pointers: q [n][H][D], k/v
+ * [n][HK][D], ao [n][H][D]. */
+int pkh_attn_prefill_batch_async(const pkh_kv_batch_t* kvb, const pkh_rope_t* rope,
+                                 int seq, int layer, int pos0, int n_tokens,
+                                 int n_heads, const float* d_q, const float* d_k,
+                                 const float* d_v, float* d_ao, void* stream);
 
 /* Copy n_pos rows of sequence `seq` of one layer between host and device
  * (dir 0: device -> host, 1: host -> device); host rows as for

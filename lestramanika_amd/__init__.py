@@ -126,6 +126,9 @@ _SIGS = {
     "pkh_attn_decode_batch_async": (_I, [ctypes.POINTER(KVBatch), ctypes.POINTER(Rope),
                                          _P, _I, _P, _P, _P, _P, _P]),
     "pkh_kv_batch_copy_rows": (_I, [ctypes.POINTER(KVBatch), _I, _I, _I, _I, _I, _P, _I]),
+    "pkh_plan_update": (_I, [_P, ctypes.POINTER(_I), _P]),
+    "pkh_attn_prefill_batch_async": (_I, [ctypes.POINTER(KVBatch), ctypes.POINTER(Rope), _I, _I,
+                                          _I, _I, _I, _P, _P, _P, _P, _P]),
     "pkh_attn_decode_noalloc_async": (_I, [ctypes.POINTER(KV), ctypes.POINTER(Rope), _I, _I, _I,
                                            _P, _P, _P, _P, _P]),
     "pkh_tune_decode_chunk": (_I, [_I]),

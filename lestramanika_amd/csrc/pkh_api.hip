@@ -594,6 +594,36 @@ extern "C" void pkh_kv_batch_free(pkh_kv_batch_t* kvb) {
     std::memset(kvb, 0, sizeof(*kvb));
 }
 
+extern "C" int pkh_attn_prefill_batch_async(const pkh_kv_batch_t* kvb, const pkh_rope_t* rope,
+                                            int seq, int layer, int pos0, int n_tokens, int n_heads,
+                                            const float* d_q, const float* d_k, const float* d_v,
+                                            float* d_ao, void* stream) {
+    if (!kvb || !kvb->k || !kvb->v) return PKH_ERR_ARG;
+    if (seq < 0 || seq >= kvb->n_seqs) return PKH_ERR_RANGE;
+    // Sequence seq's slots as a single-sequence cache: same strides, its
+    // own base and capacity.
+    pkh_kv_t kv{};
+    const size_t es = elem_size(kvb->dtype);
+    const size_t base = (size_t)kvb->slot0[seq] * kvb->stride_pos * es;
+    kv.n_layers = kvb->n_layers;
+    kv.n_kv_heads = kvb->n_kv_heads;
+    kv.head_dim = kvb->head_dim;
+    kv.max_seq = kvb->max_seq[seq];
+    kv.k_stride_layer = kvb->layer_stride;
+    kv.v_stride_layer = kvb->layer_stride;
+    kv.k = (char*)kvb->k + base;
+    kv.v = (char*)kvb->v + base;
+    kv.dtype = kvb->dtype;
+    kv.device = kvb->device;
+    kv.stride_pos = kvb->stride_pos;
+    kv.stride_head = kvb->stride_head;
+    int rc = prefill_validate(&kv, rope, layer, pos0, n_tokens, n_heads);
+    if (rc != PKH_OK) return rc;
+    if (!d_q || !d_k || !d_v || !d_ao) return PKH_ERR_ARG;
+    return prefill_checked(&kv, rope, layer, pos0, n_tokens, n_heads, d_q, d_k, d_v, d_ao,
+                           (hipStream_t)stream);
+}
+
 extern "C" int pkh_kv_batch_copy_rows(const pkh_kv_batch_t* kvb, int which_v, int layer, int seq,
                                       int pos0, int n_pos, void* host, int dir) {
     if (!kvb || !kvb->k || !host || n_pos < 0) return PKH_ERR_ARG;
@@ -621,12 +651,16 @@ extern "C" int pkh_plan_create(const pkh_kv_batch_t* kvb, const int* pos, int n_
         if (pos[s] > max_pos) max_pos = pos[s];
     }
     const int chunk = decode_chunk_for(D, n_heads, HK, kvb->dtype, rows, max_attend);
+    // Work-item slots for each sequence's whole capacity, so that later
+    // positions (pkh_plan_update) fit the same grid; a step uses as many as
+    // its position needs.
     std::vector<int> cstart((size_t)n + 1, 0);
     int max_chunks = 0;
     for (int s = 0; s < n; s++) {
-        const int c = (pos[s] + 1 + chunk - 1) / chunk;
-        cstart[s + 1] = cstart[s] + c;
-        if (c > max_chunks) max_chunks = c;
+        const long long c = ((long long)kvb->max_seq[s] + chunk - 1) / chunk;
+        if (cstart[s] + c > 0x7fffffffLL / 64) return PKH_ERR_ARG;   // grid
+        cstart[s + 1] = cstart[s] + (int)c;
+        if (c > max_chunks) max_chunks = (int)c;
     }
     pkh_plan* p = (pkh_plan*)std::calloc(1, sizeof(pkh_plan));
     if (!p) return PKH_ERR_MEMORY;
@@ -650,6 +684,19 @@ extern "C" int pkh_plan_create(const pkh_kv_batch_t* kvb, const int* pos, int n_
         return hip_fail(e, "pkh_plan_create");
     }
     *out = p;
+    return PKH_OK;
+}
+
+extern "C" int pkh_plan_update(pkh_plan_t* p, const int* pos, void* stream) {
+    if (!p || !pos) return PKH_ERR_ARG;
+    int max_pos = 0;
+    for (int s = 0; s < p->n_seqs; s++) {
+        if (pos[s] < 0 || pos[s] >= p->kvb->max_seq[s]) return PKH_ERR_RANGE;
+        if (pos[s] > max_pos) max_pos = pos[s];
+    }
+    PKH_HIP(hipMemcpyAsync(p->d_pos, pos, (size_t)p->n_seqs * sizeof(int), hipMemcpyHostToDevice,
+                           (hipStream_t)stream));
+    p->max_pos = max_pos;
     return PKH_OK;
 }
 

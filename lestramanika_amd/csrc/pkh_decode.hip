@@ -259,9 +259,22 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         }
         seq = lo;
         c = gchunk - P.chunk_start[seq];
-        n_chunks = P.chunk_start[seq + 1] - P.chunk_start[seq];
         pos = P.seq_pos[seq];
         slot0 = P.seq_slot0[seq];
+        // The plan gives each sequence work-item slots for its whole capacity
+        // (so a graph replays with positions that advance); this step uses
+        // the first ceil((pos + 1) / chunk) of them and the rest exit.  A
+        // position outside the sequence's capacity (one the host could not
+        // check, in a replayed graph) yields NaN and writes no cache row.
+        const long long cap = P.seq_slot0[seq + 1] - slot0;
+        if (pos < 0 || pos >= cap) {
+            if (c == 0 && gc > 0)
+                for (int i = threadIdx.x; i < gc * Dr; i += 64 * WAVES)
+                    P.out[((size_t)seq * H + head0 + i / Dr) * Dr + i % Dr] = __builtin_nanf("");
+            return;
+        }
+        n_chunks = min(P.chunk_start[seq + 1] - P.chunk_start[seq], (pos + P.chunk) / P.chunk);
+        if (c >= n_chunks) return;
     } else {
         seq = 0;
         c = blockIdx.x;
