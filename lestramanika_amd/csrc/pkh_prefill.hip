@@ -264,27 +264,39 @@ __device__ void exact_row(const StageParams& P, int e, float* lds) {
         }
     }
     __syncthreads();
-    // Scores, one thread per (head, key).
-    for (int t = tid; t < kExactSlot * kExactKeys; t += NT) {
-        const int h = t / kExactKeys, k = t % kExactKeys;
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int d = 0; d < D; d++) acc = fmaf(qs[h * D + d], ks[k * (D + 1) + d], acc);
-        sc[t] = acc;
+    // Scores: two threads per (head, key), each over half of the width with
+    // four independent partial sums, the halves added through a lane swap
+    // (short dependency chains: these rows are a latency chain beside the
+    // bandwidth-bound staging).
+    static_assert(NT == 2 * kExactSlot * kExactKeys, "two threads per (head, key)");
+    {
+        constexpr int DH = D / 2;
+        const int pr = tid >> 1, part = tid & 1;
+        const int h = pr / kExactKeys, k = pr % kExactKeys;
+        const float* qh = qs + h * D + part * DH;
+        const float* kh = ks + k * (D + 1) + part * DH;
+        float a4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int d = 0; d < DH; d++) a4[d & 3] = fmaf(qh[d], kh[d], a4[d & 3]);
+        float acc = (a4[0] + a4[1]) + (a4[2] + a4[3]);
+        acc += __shfl_xor(acc, 1);
+        if (part == 0) sc[pr] = acc;
     }
     __syncthreads();
-    // Softmax over keys [0, pos], one thread per head; weights over the sum.
-    if (tid < kExactSlot) {
-        float m = -INFINITY;
-        for (int k = 0; k < nk; k++) m = fmaxf(m, sc[tid * kExactKeys + k]);
-        float l = 0.0f;
-        for (int k = 0; k < kExactKeys; k++) {
-            const float w = k < nk ? __builtin_amdgcn_exp2f(sc[tid * kExactKeys + k] - m) : 0.0f;
-            sc[tid * kExactKeys + k] = w;
-            l += w;
-        }
-        const float inv = 1.0f / l;
-        for (int k = 0; k < kExactKeys; k++) sc[tid * kExactKeys + k] *= inv;
+    // Softmax over keys [0, pos]: one thread per (head, key), the head's 16
+    // keys in 16 neighbouring lanes; maximum and sum by lane exchanges.
+    if (tid < kExactSlot * kExactKeys) {
+        static_assert(kExactKeys == 16, "a head's keys fill a 16-lane group");
+        const int k = tid % kExactKeys;
+        const float sk = k < nk ? sc[tid] : -INFINITY;
+        float m = sk;
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float w = k < nk ? __builtin_amdgcn_exp2f(sk - m) : 0.0f;
+        float l = w;
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+        sc[tid] = w * (1.0f / l);
     }
     __syncthreads();
     for (int idx = tid; idx < kExactSlot * D; idx += NT) {
@@ -322,11 +334,15 @@ __global__ __launch_bounds__(kThreads) void prefill_stage(StageParams P) {
 
     const int tid = threadIdx.x;
     constexpr int SPLIT = TL::KT / RW;
-    if ((int)blockIdx.y >= P.T * SPLIT) {
-        exact_row<D, CT, kThreads>(P, ((int)blockIdx.y - P.T * SPLIT) * (int)gridDim.x + (int)blockIdx.x, lds);
+    // The exact rows' grid rows come first, so that their latency chain runs
+    // beside the staging instead of after it.
+    const int NE = (int)gridDim.y - P.T * SPLIT;
+    if ((int)blockIdx.y < NE) {
+        exact_row<D, CT, kThreads>(P, (int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x, lds);
         return;
     }
-    const int j = blockIdx.y / SPLIT, r0 = (blockIdx.y % SPLIT) * RW, g = blockIdx.x;
+    const int yb = (int)blockIdx.y - NE;
+    const int j = yb / SPLIT, r0 = (yb % SPLIT) * RW, g = blockIdx.x;
     _Float16* tk = P.tiles + ((size_t)g * P.T + j) * TL::ELEMS;
     _Float16* tv = tk + TL::K_ELEMS;
     CT* kc = static_cast<CT*>(P.k_layer) + (size_t)g * P.stride_head;
@@ -439,11 +455,15 @@ __global__ __launch_bounds__(kThreads) void prefill_stage_any(StageParams P) {
     __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
     auto sv = reinterpret_cast<_Float16 (*)[D + 4]>(lds);
     const int tid = threadIdx.x;
-    if ((int)blockIdx.y >= P.T * SPLIT) {
-        exact_row<D, CT, kThreads>(P, ((int)blockIdx.y - P.T * SPLIT) * (int)gridDim.x + (int)blockIdx.x, lds);
+    // The exact rows' grid rows come first, so that their latency chain runs
+    // beside the staging instead of after it.
+    const int NE = (int)gridDim.y - P.T * SPLIT;
+    if ((int)blockIdx.y < NE) {
+        exact_row<D, CT, kThreads>(P, (int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x, lds);
         return;
     }
-    const int j = blockIdx.y / SPLIT, r0 = (blockIdx.y % SPLIT) * RW, g = blockIdx.x;
+    const int yb = (int)blockIdx.y - NE;
+    const int j = yb / SPLIT, r0 = (yb % SPLIT) * RW, g = blockIdx.x;
     const int Dr = P.Dr;
     _Float16* tk = P.tiles + ((size_t)g * P.T + j) * TL::ELEMS;
     _Float16* tv = tk + TL::K_ELEMS;
@@ -1125,8 +1145,8 @@ int launch_dg(const PrefillArgs& a, int nsub, hipStream_t st) {
     const long long rows = (long long)a.pos0 + a.n_tokens;
     const int T = (int)((rows + TL::KT - 1) / TL::KT);
     const int HK = a.n_kv_heads;
-    // Rows below kExactKeys: n_exact * nsub extra grid rows of HK workgroups,
-    // one per (row, head slot).
+    // Rows below kExactKeys: n_exact * nsub extra grid rows (the first ones)
+    // of HK workgroups, one per (row, head slot).
     const int n_exact = std::max(0, std::min(a.n_tokens, kExactKeys - a.pos0));
     if ((long long)T * (TL::KT / StageRows<D>::N) + (long long)n_exact * nsub > 65535)
         return PKH_ERR_ARG;                                                       // grid y limit
