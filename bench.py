@@ -302,6 +302,26 @@ def run_decode(args, cfg):
     avg_launch = float(durs.mean())
     achieved = bpl / avg_launch / 1e9
 
+    # The floor under one layer call on this box: the same replay of a
+    # graph of L dependent launches of a one-element kernel, per launch.
+    x1 = torch.zeros(1, device=dev)
+    floor_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(floor_graph):
+        for _ in range(L):
+            x1.add_(1.0)
+    for _ in range(args.warmup):
+        floor_graph.replay()
+    torch.cuda.synchronize()
+    fevs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(args.steps)]
+    for e0, e1 in fevs:
+        e0.record(stream)
+        floor_graph.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    node_us = float(np.mean([e0.elapsed_time(e1) for e0, e1 in fevs])) * 1e3 / L
+    log(f"bench: graph node floor {node_us:.3f} us (one-element kernel, {L} nodes per graph)")
+
     # The host-pointer entry the seam binding uses (pkh_attn_decode with q, k,
     # v and ao in pageable host memory, as the reference's state buffers
     # are): one packed upload, the kernel, one download per layer call.  PCIe
@@ -383,6 +403,7 @@ def run_decode(args, cfg):
                    "rope_theta": cfg["theta"], "new_token_pos": ctx},
         "us_per_layer_step": round(wall / n_launch * 1e6, 3),
         "eager_us_per_layer_step": round(eager_wall / n_launch * 1e6, 3),
+        "graph_node_floor_us": round(node_us, 3),
         "host_entry_us_per_layer_step": round(host_us, 2),
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "bytes_per_layer_step": bpl,
