@@ -518,6 +518,14 @@ struct AttnParams {
     int Dr;                     // real head_dim
     int nsub;                   // head slots per KV head
     float qscale;               // log2(e) / sqrt(Dr)
+    // Keys split over workgroups: nsplit workgroups per (query block, head
+    // slot), split s taking tiles [s*tps, (s+1)*tps) of its causal range.
+    // With nsplit > 1 each writes its unnormalised partial (o, and the
+    // column's m and l) to part_o [nsplit][nqb][slot][kCols][D] and part_ml
+    // [nsplit][nqb][slot][kCols][2], and prefill_merge finishes the rows.
+    int nsplit, tps;
+    float* part_o;
+    float* part_ml;
 };
 
 __device__ __forceinline__ float max_halves(float x) {
@@ -593,7 +601,7 @@ template <int D> struct Groups { static constexpr int N = D >= 256 ? 1 : 2; };
 constexpr int kSlots = 4;        // K ring and V ring depth
 constexpr int kCols = 128;       // query columns per workgroup
 
-template <int D, int G, bool PAD>
+template <int D, int G, bool PAD, bool SPLIT>
 __global__ __launch_bounds__(256 * Groups<D>::N)
 __attribute__((amdgpu_waves_per_eu(Groups<D>::N, Groups<D>::N)))
 void prefill_attn(AttnParams P) {
@@ -629,19 +637,33 @@ void prefill_attn(AttnParams P) {
     const int gc = min(G, (g * P.H + P.H + P.HK - 1) / P.HK - head0);
     if (gc <= 0) return;                                      // a KV head that serves no query head
     const int Dr = PAD ? P.Dr : D;
-    const int qb = P.nqb - 1 - (int)(blockIdx.x / NY);        // longest first
+    const int rest = (int)(blockIdx.x / NY);
+    const int split = rest % P.nsplit;                        // key range of this workgroup
+    const int qb = P.nqb - 1 - rest / P.nsplit;               // longest first
     const int qmin_wg = P.pos0 + qb * BM;
     const int qmax = P.pos0 + min(qb * BM + BM - 1, P.n - 1);
-    const int ntile = qmax / KT + 1;
+    const int tbase = split * P.tps;                          // first tile of the range
+    const int ntile = min(qmax / KT + 1 - tbase, P.tps);      // tiles in the range
+    const size_t pbase = (((size_t)split * P.nqb + qb) * NY + y) * kCols;   // partial rows
+    if (SPLIT && ntile <= 0) {
+        // A range past this block's causal extent: an empty partial.
+        for (int c = threadIdx.x; c < kCols; c += blockDim.x) {
+            P.part_ml[(pbase + c) * 2 + 0] = -INFINITY;
+            P.part_ml[(pbase + c) * 2 + 1] = 0.0f;
+        }
+        return;
+    }
 
     // This KV head's tiles as one buffer (reads past its end return zero).
     const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<_Float16*>(P.tiles + (size_t)g * P.T * TL::ELEMS), (short)0, P.T * TL::BYTES, 0x00020000);
+    // Tile t of the loop below is tile tbase + t of the KV head.
     auto load_k = [&](_Float16* dst, int t) __attribute__((always_inline)) {
-        copy_to_lds<TL::K_ELEMS * 2, kAttnWaves>(dst, trs, (unsigned)(t * TL::BYTES), w, lane);
+        copy_to_lds<TL::K_ELEMS * 2, kAttnWaves>(dst, trs, (unsigned)((tbase + t) * TL::BYTES), w, lane);
     };
     auto load_v = [&](_Float16* dst, int t) __attribute__((always_inline)) {
-        copy_to_lds<TL::V_ELEMS * 2, kAttnWaves>(dst, trs, (unsigned)(t * TL::BYTES + TL::K_ELEMS * 2), w, lane);
+        copy_to_lds<TL::V_ELEMS * 2, kAttnWaves>(dst, trs, (unsigned)((tbase + t) * TL::BYTES + TL::K_ELEMS * 2),
+                                               w, lane);
     };
     // Tiles for the first phases (the loop's phase p issues the loads of
     // phase p + 1 at its end): K(0), K(1), K(2) and V(0) with two groups;
@@ -873,12 +895,13 @@ void prefill_attn(AttnParams P) {
     // running max (the accumulator is rescaled only when the max grows by
     // more than kTau), exp2, row sums of the fp16 weights as P^T uses them.
     auto softmax = [&](int t) __attribute__((always_inline)) {
-        if (t * KT + KT - 1 > qmin_wg) {
+        const int tg = tbase + t;                  // the KV head's tile index
+        if (tg * KT + KT - 1 > qmin_wg) {
 #pragma unroll
             for (int kb = 0; kb < NKB; kb++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int key = t * KT + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    const int key = tg * KT + kb * 32 + 8 * (r >> 2) + 4 * hh + (r & 3);
                     if (key > qpos) S[kb][r] = -INFINITY;
                 }
         }
@@ -1058,9 +1081,25 @@ void prefill_attn(AttnParams P) {
         const float M = fmaxf(m_run, mb);
         fa = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
         fb = mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb - M);
-        inv = 1.0f / sum_halves(l_run * fa + lb * fb);
+        const float L = sum_halves(l_run * fa + lb * fb);
+        inv = 1.0f / L;
+        if constexpr (SPLIT) {
+            inv = 1.0f;                            // the partial stays unnormalised
+            if (grp == 0 && hh == 0) {
+                P.part_ml[(pbase + 32 * sub + l32) * 2 + 0] = M;
+                P.part_ml[(pbase + 32 * sub + l32) * 2 + 1] = L;
+            }
+        }
     } else {
-        inv = 1.0f / sum_halves(l_run);
+        const float L = sum_halves(l_run);
+        inv = 1.0f / L;
+        if constexpr (SPLIT) {
+            inv = 1.0f;
+            if (hh == 0) {
+                P.part_ml[(pbase + 32 * sub + l32) * 2 + 0] = m_run;
+                P.part_ml[(pbase + 32 * sub + l32) * 2 + 1] = L;
+            }
+        }
     }
     if constexpr (NG == 2) {
         // Owned block b: read the partner's partial (4 KB of xbuf(b) per
@@ -1097,7 +1136,9 @@ void prefill_attn(AttnParams P) {
                 const int cg = 32 * sub + c;
                 const int tc = qb * BM + cg / G;
                 const int d = 32 * b + 4 * u;
-                if (tc < P.n && cg % G < gc && d < Dr && P.pos0 + tc >= kExactKeys) {
+                if constexpr (SPLIT) {
+                    if (d < D) *reinterpret_cast<float4*>(P.part_o + (pbase + cg) * D + d) = o;
+                } else if (tc < P.n && cg % G < gc && d < Dr && P.pos0 + tc >= kExactKeys) {
                     float* orow = P.out + ((size_t)tc * P.H + head0 + cg % G) * Dr;
                     if constexpr (PAD) {
                         const float ov[4] = {o.x, o.y, o.z, o.w};
@@ -1111,6 +1152,16 @@ void prefill_attn(AttnParams P) {
                 }
             }
         }
+        return;
+    }
+    if constexpr (SPLIT) {
+        float* prow = P.part_o + (pbase + col) * D;
+#pragma unroll
+        for (int b = 0; b < NDB; b++)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; r4++)
+                *reinterpret_cast<float4*>(prow + 32 * b + 8 * r4 + 4 * hh) =
+                    make_float4(acc[b][4 * r4 + 0], acc[b][4 * r4 + 1], acc[b][4 * r4 + 2], acc[b][4 * r4 + 3]);
         return;
     }
     if (!valid || P.pos0 + ti < kExactKeys) return;   // rows written by the staging kernel
@@ -1137,6 +1188,91 @@ void prefill_attn(AttnParams P) {
     }
 }
 
+// ---- merge of the key splits -----------------------------------------------
+
+// One thread per (query block, head slot, column, 4 elements of the width):
+// the nsplit partials of the column merged with their maxima, normalised,
+// written to the column's row (rows below kExactKeys are the staging
+// kernel's).  A split with m = -inf (no keys) counts for nothing.
+template <int D, int G, bool PAD>
+__global__ __launch_bounds__(256) void prefill_merge(AttnParams P) {
+    constexpr int BM = kCols / G;
+    constexpr int NV = D / 4;
+    const int NY = P.HK * P.nsub;
+    const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int v4 = (int)(t % NV);
+    long long r = t / NV;
+    const int col = (int)(r % kCols);
+    r /= kCols;
+    const int y = (int)(r % NY);
+    const int qb = (int)(r / NY);
+    if (qb >= P.nqb) return;
+    const int g = y / P.nsub;
+    const int ysub = y - g * P.nsub;
+    const int head0 = (g * P.H + P.HK - 1) / P.HK + ysub * G;
+    const int gc = min(G, (g * P.H + P.H + P.HK - 1) / P.HK - head0);
+    const int tc = qb * BM + col / G;
+    const int Dr = PAD ? P.Dr : D;
+    const int d = 4 * v4;
+    if (gc <= 0 || tc >= P.n || col % G >= gc || P.pos0 + tc < kExactKeys || d >= Dr) return;
+    const size_t stride = (size_t)P.nqb * NY * kCols;           // one split's rows
+    const size_t row = ((size_t)qb * NY + y) * kCols + col;
+    // Batches of 8 splits, every load of a batch issued before any is used
+    // (one memory round trip per batch), folded online.  The o of an empty
+    // split was never written: it is selected away, not multiplied by 0.
+    constexpr int NB = 8;
+    float M = -INFINITY, L = 0.0f;
+    float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s0 = 0; s0 < P.nsplit; s0 += NB) {
+        float2 ml[NB];
+        float4 o[NB];
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const size_t r2 = (size_t)min(s0 + i, P.nsplit - 1) * stride + row;
+            ml[i] = *reinterpret_cast<const float2*>(P.part_ml + r2 * 2);
+            o[i] = *reinterpret_cast<const float4*>(P.part_o + r2 * D + d);
+            if (s0 + i >= P.nsplit) ml[i].x = -INFINITY;
+        }
+        float mb = M;
+#pragma unroll
+        for (int i = 0; i < NB; i++) mb = fmaxf(mb, ml[i].x);
+        const float a = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - mb);
+        L *= a;
+        O.x *= a;
+        O.y *= a;
+        O.z *= a;
+        O.w *= a;
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const bool live = ml[i].x != -INFINITY;
+            const float w = live ? __builtin_amdgcn_exp2f(ml[i].x - mb) : 0.0f;
+            L = live ? fmaf(ml[i].y, w, L) : L;
+            O.x = live ? fmaf(o[i].x, w, O.x) : O.x;
+            O.y = live ? fmaf(o[i].y, w, O.y) : O.y;
+            O.z = live ? fmaf(o[i].z, w, O.z) : O.z;
+            O.w = live ? fmaf(o[i].w, w, O.w) : O.w;
+        }
+        M = mb;
+    }
+    const float inv = 1.0f / L;
+    float* orow = P.out + ((size_t)tc * P.H + head0 + col % G) * Dr;
+    const float ov[4] = {O.x * inv, O.y * inv, O.z * inv, O.w * inv};
+    if constexpr (PAD) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (d + e < Dr) orow[d + e] = ov[e];
+    } else {
+        *reinterpret_cast<float4*>(orow + d) = make_float4(ov[0], ov[1], ov[2], ov[3]);
+    }
+}
+
+// Key splits per query block: a launch with few query blocks (a prompt chunk
+// after a long context) gets about kSplitTarget workgroups, each over at
+// least kMinSplitTiles tiles, since a workgroup's fixed cost (q prologue,
+// merge, output) is worth several tiles.
+constexpr int kSplitTarget = 256;
+constexpr int kMinSplitTiles = 8;
+
 // ---- launch ----------------------------------------------------------------
 
 template <int D, int G, typename CT>
@@ -1154,10 +1290,23 @@ int launch_dg(const PrefillArgs& a, int nsub, hipStream_t st) {
     if ((long long)T * TL::BYTES >= (1LL << 31)) return PKH_ERR_ARG;
     constexpr int BM = kCols / G;
     const long long nqb = (a.n_tokens + BM - 1) / BM;
-    if (nqb * HK * nsub > 0x7fffffffLL) return PKH_ERR_ARG;                     // grid x limit
+    const long long base_wgs = nqb * HK * nsub;
+    int nsplit = 1, tps = T;
+    if (base_wgs < kSplitTarget && T >= 2 * kMinSplitTiles) {
+        nsplit = (int)std::min<long long>(kSplitTarget / base_wgs, T / kMinSplitTiles);
+        tps = (T + nsplit - 1) / nsplit;
+        nsplit = (T + tps - 1) / tps;
+    }
+    if (base_wgs * nsplit > 0x7fffffffLL) return PKH_ERR_ARG;                   // grid x limit
     void* tiles = nullptr;
     int rc = tiles_get((size_t)HK * T * TL::BYTES, &tiles);
     if (rc != PKH_OK) return rc;
+    void* parts = nullptr;
+    const size_t part_rows = (size_t)nsplit * nqb * HK * nsub * kCols;
+    if (nsplit > 1) {
+        rc = scratch_get(part_rows * (D + 2) * sizeof(float), &parts);
+        if (rc != PKH_OK) return rc;
+    }
 
     // The vector staging needs whole 4-element groups on both sides of the
     // rotation half and 16-byte aligned new rows: the real width D itself.
@@ -1209,12 +1358,32 @@ int launch_dg(const PrefillArgs& a, int nsub, hipStream_t st) {
     A.Dr = a.head_dim;
     A.nsub = nsub;
     A.qscale = (1.0f / sqrtf((float)a.head_dim)) * 1.4426950408889634f;
-    const dim3 agrid((unsigned)(nqb * HK * nsub)), ablock(256 * Groups<D>::N);
-    if (pad)
-        hipLaunchKernelGGL((prefill_attn<D, G, true>), agrid, ablock, 0, st, A);
-    else
-        hipLaunchKernelGGL((prefill_attn<D, G, false>), agrid, ablock, 0, st, A);
+    A.nsplit = nsplit;
+    A.tps = tps;
+    A.part_o = static_cast<float*>(parts);
+    A.part_ml = A.part_o ? A.part_o + part_rows * D : nullptr;
+    const dim3 agrid((unsigned)(base_wgs * nsplit)), ablock(256 * Groups<D>::N);
+    if (nsplit > 1) {
+        if (pad)
+            hipLaunchKernelGGL((prefill_attn<D, G, true, true>), agrid, ablock, 0, st, A);
+        else
+            hipLaunchKernelGGL((prefill_attn<D, G, false, true>), agrid, ablock, 0, st, A);
+    } else {
+        if (pad)
+            hipLaunchKernelGGL((prefill_attn<D, G, true, false>), agrid, ablock, 0, st, A);
+        else
+            hipLaunchKernelGGL((prefill_attn<D, G, false, false>), agrid, ablock, 0, st, A);
+    }
     PKH_HIP(hipGetLastError());
+    if (nsplit > 1) {
+        const long long nthreads = base_wgs * kCols * (D / 4);
+        const dim3 mgrid((unsigned)((nthreads + 255) / 256));
+        if (pad)
+            hipLaunchKernelGGL((prefill_merge<D, G, true>), mgrid, dim3(256), 0, st, A);
+        else
+            hipLaunchKernelGGL((prefill_merge<D, G, false>), mgrid, dim3(256), 0, st, A);
+        PKH_HIP(hipGetLastError());
+    }
 
     return PKH_OK;
 }

@@ -108,6 +108,25 @@ def test_prefill_tinyllama_after_context():
     _check_free(32, 4, 64, 1500, 300, 1e4, 51)
 
 
+def test_prefill_chunk_after_long_context():
+    """A 128-token prompt chunk after 8192 cached rows (Llama-3-8B shape): 32
+    query blocks' worth of workgroups, so each block's keys are split over
+    several workgroups and merged."""
+    ao, ref = _check_free(32, 8, 128, 8192, 128, 5e5, 81)
+    log(f"chunk after 8192 rows: max-abs err {maxerr(ao, ref):.3e}")
+
+
+@pytest.mark.parametrize("case", [(4, 1, 64, 0, 1024), (4, 1, 256, 1000, 64), (8, 2, 80, 2000, 40),
+                                  (12, 2, 32, 500, 150)],
+                         ids=["empty-ranges", "D256", "D80", "G6"])
+def test_prefill_key_splits(case):
+    """Key splits: ranges past a block's causal extent (the first query
+    blocks of a 1024-token prompt from 0), the one-group kernel of head_dim
+    256, a padded width and an uneven group."""
+    H, HK, D, pos0, n = case
+    _check_free(H, HK, D, pos0, n, 1e4, 90 + D + pos0 + n)
+
+
 @pytest.mark.parametrize("D,G", [(16, 2), (64, 8), (128, 4), (256, 1)])
 def test_prefill_fp16_kv(D, G):
     for pos0, n in ((0, 50), (300, 97)):
