@@ -807,7 +807,8 @@ def main():
                     choices=sorted(WORKLOADS) + sorted(PREFILL_WORKLOADS) + sorted(RAGGED_WORKLOADS)
                     + ["copy-calibration"])
     ap.add_argument("--no-secondary", action="store_true",
-                    help="skip the prefill and ragged measurements appended to the decode line")
+                    help="skip the prefill, chunked-prefill and ragged measurements appended to "
+                         "the decode line")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=32,
                     help="layers in the CPU-baseline sample")
@@ -832,6 +833,7 @@ def main():
                     "config", "dtype")
             res["secondary"] = {}
             for name, fn, table in (("llama3-8b-prefill-2048", run_prefill, PREFILL_WORKLOADS),
+                                    ("llama3-8b-prefill-chunk128-ctx8192", run_prefill, PREFILL_WORKLOADS),
                                     ("llama3-8b-ragged16-fp16", run_ragged, RAGGED_WORKLOADS)):
                 torch.cuda.empty_cache()
                 sec = fn(args, table[name], name)
