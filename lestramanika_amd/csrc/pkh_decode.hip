@@ -242,7 +242,13 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     const int grp = lane / LPP;      // row of the tile handled by this lane
     const int H = P.H, HK = P.HK, half = P.half;
     const int Dr = PAD ? P.Dr : D;
-    const int y = blockIdx.y;        // head slot
+    // One-dimensional grid, head slot fastest: on an 8-XCD part with 8 head
+    // slots each XCD streams one KV head's chunks (workgroups go to XCDs
+    // round-robin by index), and a head's merger is still its last item.
+    const int ny = P.HK * P.nsub;                        // head slots
+    const int y = (int)blockIdx.x % ny;                  // head slot
+    const int bx = (int)blockIdx.x / ny;                 // chunk index in the grid
+    const int nbx = (int)gridDim.x / ny;                 // chunks in the grid
     const int g = y / P.nsub;        // its KV head
     const int sub = y - g * P.nsub;
     const int head0 = (g * H + HK - 1) / HK + sub * G;               // first query head
@@ -251,7 +257,7 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     int seq, c, pos, n_chunks, gchunk;
     long long slot0;
     if constexpr (RAGGED) {
-        gchunk = blockIdx.x;
+        gchunk = bx;
         int lo = 0, hi = P.n_seqs;   // largest s with chunk_start[s] <= gchunk
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
@@ -277,9 +283,9 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         if (c >= n_chunks) return;
     } else {
         seq = 0;
-        c = blockIdx.x;
+        c = bx;
         gchunk = c;
-        n_chunks = gridDim.x;
+        n_chunks = nbx;
         pos = P.pos;
         slot0 = P.slot0;
     }
@@ -619,14 +625,14 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     // work item replaces a shared ticket counter, whose atomics serialize
     // when all chunks of a head finish together.
     const bool merger = c == n_chunks - 1;
-    int* const flags = P.counters + (size_t)blockIdx.y * gridDim.x;
+    int* const flags = P.counters + (size_t)y * nbx;
     __shared__ float own_o[G * D];
     __shared__ float own_m[G], own_l[G];
     if (!merger) {
         if (has_col) {
             // 8-byte device-scope atomic stores: (o[d], o[d + 1]) pairs and (m, l).
             // Partials are [chunk][slot][G][D].
-            const size_t base = ((size_t)gchunk * gridDim.y + y) * G + oh;
+            const size_t base = ((size_t)gchunk * ny + y) * G + oh;
             unsigned long long* po = reinterpret_cast<unsigned long long*>(P.part_o + base * D + od);
 #pragma unroll
             for (int e = 0; e < CW; e += 2)
@@ -642,7 +648,7 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __syncthreads();
         if (threadIdx.x == 0)
-            __hip_atomic_fetch_add(flags + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(flags + bx, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     // The merger keeps its own partial in LDS.
@@ -659,7 +665,7 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
     // a timed-out wait brings its flag back to 0, so the next launch (which
     // starts after every workgroup of this one has ended) finds all flags
     // at 0 and never takes a stale flag for its own partial.
-    const int cfirst = (int)blockIdx.x - c;     // this head's first chunk
+    const int cfirst = bx - c;     // this head's first chunk
     bool timed_out = true;
     for (int round = 0; round < P.max_polls; round++) {
         int missing = 0;
@@ -711,7 +717,7 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
             const int t = min((int)threadIdx.x + r * 64 * WAVES, CGN * B * G - 1);
             const int c = min(b0 + t / G, n_parts - 1);
             mlv[r] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
-                pmrs, (unsigned)((((size_t)(c0 + c) * gridDim.y + y) * G + t % G) * 2 * sizeof(float)), 0,
+                pmrs, (unsigned)((((size_t)(c0 + c) * ny + y) * G + t % G) * 2 * sizeof(float)), 0,
                 kCoherent));
         }
         __builtin_amdgcn_sched_barrier(0);   // the pairs go out first: their wait leaves the o blocks in flight
@@ -719,7 +725,7 @@ __attribute__((amdgpu_waves_per_eu(Shape<D, G, KT>::MINW))) void decode_split(Sp
 #pragma unroll
         for (int i = 0; i < B; i++) {
             const int c = min(b0 + cg + i * CGN, n_parts - 1);
-            const size_t base = ((size_t)(c0 + c) * gridDim.y + y) * G + h;
+            const size_t base = ((size_t)(c0 + c) * ny + y) * G + h;
             // 16-byte loads with the device-coherent (sc1) policy.
             oc[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
                 pors, (unsigned)((base * D + (4 * col) % D) * sizeof(float)), 0, kCoherent));
@@ -865,7 +871,7 @@ constexpr int kWaves = 4;
 
 template <int D, int G, typename KT>
 int launch_typed(const DecodeArgs& a, const SplitParams& P, int total_chunks, int ny, hipStream_t st) {
-    dim3 grid(total_chunks, ny), block(64 * kWaves);
+    dim3 grid((unsigned)total_chunks * (unsigned)ny), block(64 * kWaves);
     const bool ragged = a.d_chunk_start != nullptr;
     const bool pad = P.Dr != D;
 #define PKH_GO(R, PD) hipLaunchKernelGGL((decode_split<D, G, KT, kWaves, R, PD>), grid, block, 0, st, P)
@@ -1006,6 +1012,7 @@ int launch_decode(const DecodeArgs& a, hipStream_t st, bool no_alloc) {
     if ((max_rows + 1) * a.stride_pos * elem >= (1LL << 31)) return PKH_ERR_ARG;
 
     const int total_chunks = a.total_chunks;
+    if ((long long)total_chunks * ny > 0x7fffffffLL) return PKH_ERR_ARG;   // one-dimensional grid
     if (a.max_chunks > 1) {
         // Scratch: [part_o][part_ml], partials indexed [chunk][slot][G][DP];
         // one partial-ready flag per work item (chunk, head slot) in the
