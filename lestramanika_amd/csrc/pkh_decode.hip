@@ -924,7 +924,7 @@ bool shape_supported(int head_dim, int n_heads, int n_kv_heads) {
     if (n_heads <= 0 || n_kv_heads <= 0 || padded_head_dim(head_dim) == 0) return false;
     const int DP = padded_head_dim(head_dim);
     const long long ny = (long long)n_kv_heads * head_slots(n_heads, n_kv_heads, decode_gmax(DP)).nsub;
-    return ny <= 65535;   // grid y
+    return ny <= 65535;   // head slots, kept within one grid dimension
 }
 
 int decode_tile_positions(int head_dim, int dtype) {
